@@ -1,0 +1,195 @@
+/*
+ * teeny_hip.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * One function per op direction.  Each takes device pointers and scalars in
+ * the order the reference's RuntimeOp::pack_args / pack_backward_args hands
+ * them to its kernel's `entry_point` (cited per function), followed by the
+ * extensions the reference lacks (batch, GQA head counts, head_dim, dtype),
+ * an optional workspace, and the HIP stream all work is queued on.
+ *
+ * Conventions
+ *   - Every pointer is device memory owned by the caller.  Functions never
+ *     allocate device memory, never synchronise the device, and return as
+ *     soon as the work is queued on `stream` (0 = the null stream).
+ *   - Layouts are the reference's: attention tensors [B*H, S, D] contiguous
+ *     (src/kernels/flash_attn2.rs:23), activations [rows, cols] row-major.
+ *   - dtype is TEENY_F32 (the reference's type) or TEENY_BF16 (storage; all
+ *     arithmetic is fp32, matrix products use bf16 MFMA with fp32 accumulate).
+ *     LSE and rstd caches are always fp32.
+ *   - Return 0 on success or a negative TEENY_ERR_* code; shapes and
+ *     pointers are validated before anything is launched, nothing aborts.
+ *   - Thread safety: every entry point is re-entrant; code objects are loaded
+ *     once per device on first use (or by teeny_init) under a lock.
+ */
+#ifndef TEENY_HIP_H
+#define TEENY_HIP_H
+
+#include <stddef.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TEENY_ABI_VERSION 1
+
+typedef enum { TEENY_F32 = 0, TEENY_BF16 = 1, TEENY_I32 = 2 } teeny_dtype;
+
+#define TEENY_OK 0
+#define TEENY_ERR_NULL_POINTER (-1)   /* a required pointer is NULL */
+#define TEENY_ERR_INVALID_SHAPE (-2)  /* a size is <= 0, inconsistent, or too large */
+#define TEENY_ERR_UNSUPPORTED (-3)    /* dtype / head_dim combination not built */
+#define TEENY_ERR_WORKSPACE (-4)      /* workspace missing or smaller than required */
+#define TEENY_ERR_HIP (-5)            /* a HIP runtime call failed (teeny_last_hip_error) */
+#define TEENY_ERR_MODULE (-6)         /* code object or kernel symbol could not be loaded */
+#define TEENY_ERR_INVALID_VALUE (-7)  /* a scalar argument is out of its domain */
+
+/* Library version, error text, last HIP error seen by this thread. */
+int teeny_abi_version(void);
+const char* teeny_strerror(int code);
+int teeny_last_hip_error(void);
+
+/* Load the code objects on the current device (optional: done lazily). */
+int teeny_init(void);
+
+/* --------------------------------------------------------------------------
+ * Flash attention 2
+ *
+ * q [B*Hq, n_ctx_q, D], k/v [B*Hkv, n_ctx_k, D], o [B*Hq, n_ctx_q, D],
+ * l (LSE cache, the RuntimeOp's param slot 0) [B*Hq, n_ctx_q] fp32.
+ * LSE is natural-log in the scaled-score domain: m + ln(l)
+ * (src/kernels/flash_attn2.rs:120-122).  Causal masks key > query, top-left
+ * aligned (flash_attn2.rs:104-107).  q head h uses kv head h / (Hq / Hkv).
+ * head_dim: fp32 8, 16, 32, 64, 128; bf16 64, 128.
+ * neg_inf must be -INFINITY (the only value the reference passes,
+ * flash_attn2.rs:478, :331).
+ * ------------------------------------------------------------------------ */
+
+/* Replaces CausalFlashAttn2RuntimeOp::pack_args + launch
+ * (src/kernels/flash_attn2.rs:459-487): (q, k, v, o, l, n_ctx_q, n_ctx_k,
+ * softmax_scale, neg_inf). */
+int teeny_causal_flash_attn2_fwd(const void* q, const void* k, const void* v, void* o, float* l,
+                                 int n_ctx_q, int n_ctx_k, float softmax_scale, float neg_inf,
+                                 int batch, int n_heads_q, int n_heads_kv, int head_dim,
+                                 int dtype, hipStream_t stream);
+
+/* Replaces FlashAttn2RuntimeOp::pack_args + launch (flash_attn2.rs:309-340),
+ * the bidirectional forward; same arguments. */
+int teeny_flash_attn2_fwd(const void* q, const void* k, const void* v, void* o, float* l,
+                          int n_ctx_q, int n_ctx_k, float softmax_scale, float neg_inf,
+                          int batch, int n_heads_q, int n_heads_kv, int head_dim, int dtype,
+                          hipStream_t stream);
+
+/* Replaces CausalFlashAttn2RuntimeOp::pack_backward_args + launch
+ * (flash_attn2.rs:493-529): (q, k, v, o, do, l, dq, dk, dv, n_ctx_q, n_ctx_k,
+ * softmax_scale).  dq, dk and dv are overwritten: unlike the reference
+ * (flash_attn2.rs:35) they need no zero initialisation.  dk/dv of a GQA kv
+ * head are the sums over its q heads.  workspace: at least
+ * teeny_flash_attn2_bwd_workspace_bytes(...) bytes of device memory. */
+int teeny_causal_flash_attn2_bwd(const void* q, const void* k, const void* v, const void* o,
+                                 const void* dout, const float* l, void* dq, void* dk, void* dv,
+                                 int n_ctx_q, int n_ctx_k, float softmax_scale, int batch,
+                                 int n_heads_q, int n_heads_kv, int head_dim, int dtype,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Replaces FlashAttn2RuntimeOp::pack_backward_args + launch
+ * (flash_attn2.rs:346-383), the bidirectional backward; same arguments. */
+int teeny_flash_attn2_bwd(const void* q, const void* k, const void* v, const void* o,
+                          const void* dout, const float* l, void* dq, void* dk, void* dv,
+                          int n_ctx_q, int n_ctx_k, float softmax_scale, int batch, int n_heads_q,
+                          int n_heads_kv, int head_dim, int dtype, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace the backward needs: Delta [B*Hq, n_ctx_q] fp32, plus for bf16 a
+ * dQ accumulator [B*Hq, n_ctx_q, D] fp32.  No counterpart in the reference
+ * (its executor sizes caches from RuntimeOp::param_shapes, flash_attn2.rs:449-457). */
+size_t teeny_flash_attn2_bwd_workspace_bytes(int n_ctx_q, int batch, int n_heads_q, int head_dim,
+                                             int dtype);
+
+/* --------------------------------------------------------------------------
+ * RoPE on x [BH, n_ctx, head_dim], interleaved pairs, position = row index.
+ * Replaces RopeRtOp::pack_args (src/kernels/rope.rs:180-204): (x, y, n_ctx,
+ * ln_rope_base) and pack_backward_args (:210-237): (dy, dx, n_ctx,
+ * ln_rope_base).  head_dim even; a multiple of 4 (fp32) or 8 (bf16).
+ * In-place (y == x) is allowed.
+ * ------------------------------------------------------------------------ */
+int teeny_rope_fwd(const void* x, void* y, int n_ctx, float ln_rope_base, int bh, int head_dim,
+                   int dtype, hipStream_t stream);
+int teeny_rope_bwd(const void* dy, void* dx, int n_ctx, float ln_rope_base, int bh, int head_dim,
+                   int dtype, hipStream_t stream);
+
+/* --------------------------------------------------------------------------
+ * Head transposes, byte-exact.
+ * transpose_heads: src [B, S, H*Dh] -> dst [B, H, S, Dh].  Replaces
+ *   TransposeHeads RuntimeOp::pack_args (src/kernels/transpose_heads.rs:106-129):
+ *   (src, dst, seq_len, n_heads).
+ * merge_heads: src [B, H, S, Dh] -> dst [B, S, H*Dh].  Replaces MergeHeads
+ *   RuntimeOp::pack_args (transpose_heads.rs:214-237).
+ * Each is the other's backward (transpose_heads.rs:146-154, :256-264).
+ * ------------------------------------------------------------------------ */
+int teeny_transpose_heads(const void* src, void* dst, int seq_len, int n_heads, int batch,
+                          int head_dim, int dtype, hipStream_t stream);
+int teeny_merge_heads(const void* src, void* dst, int seq_len, int n_heads, int batch,
+                      int head_dim, int dtype, hipStream_t stream);
+
+/* --------------------------------------------------------------------------
+ * Fused residual add + RMSNorm over rows of N.
+ * fwd replaces FusedAddRmsnormRtOp::pack_args (src/kernels/fused_add_rmsnorm.rs:227-254):
+ *   (x, residual, y, h, rstd, weight, M, N, eps); h = x + residual (param
+ *   slot 1), rstd [M] fp32 (param slot 2), weight [N] (slot 0).
+ * bwd replaces pack_backward_args (fused_add_rmsnorm.rs:260-291):
+ *   (dy, h, dx, dresidual, dweight, weight, rstd, M, N); dweight is
+ *   ACCUMULATED into (dweight += sum over rows), as in the reference
+ *   (fused_add_rmsnorm.rs:187), but deterministically.  dresidual may be NULL.
+ *   workspace: teeny_fused_add_rmsnorm_bwd_workspace_bytes(M, N).
+ * rmsnorm_fwd: the plain norm the Llama block records (src/layers/mod.rs:61-65);
+ *   rstd may be NULL.
+ * rmsnorm_bwd: backward of that plain norm with the true gradient
+ *   dx = rstd * (w * dy - x * rstd^2 * sum(dy * w * x) / N); dweight accumulated
+ *   as above; same workspace.  The fused backward keeps the reference's
+ *   formula rstd * w * (dy - h * rstd^2 * sum(dy * w * h) / N)
+ *   (fused_add_rmsnorm.rs:184), which equals the true gradient only when
+ *   w == 1.  No reference entry point (the block's norm is teeny-core's
+ *   RmsNorm, src/layers/mod.rs:61-65, whose source is absent).
+ * N: a multiple of 8 (bf16) / 4 (fp32) up to 64*8*16, or any N up to 1024.
+ * ------------------------------------------------------------------------ */
+int teeny_fused_add_rmsnorm_fwd(const void* x, const void* residual, void* y, void* h,
+                                float* rstd, const void* weight, int M, int N, float eps,
+                                int dtype, hipStream_t stream);
+int teeny_fused_add_rmsnorm_bwd(const void* dy, const void* h, void* dx, void* dresidual,
+                                void* dweight, const void* weight, const float* rstd, int M,
+                                int N, int dtype, void* workspace, size_t workspace_bytes,
+                                hipStream_t stream);
+size_t teeny_fused_add_rmsnorm_bwd_workspace_bytes(int M, int N);
+int teeny_rmsnorm_fwd(const void* x, void* y, float* rstd, const void* weight, int M, int N,
+                      float eps, int dtype, hipStream_t stream);
+int teeny_rmsnorm_bwd(const void* dy, const void* x, void* dx, void* dweight, const void* weight,
+                      const float* rstd, int M, int N, int dtype, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream);
+
+/* --------------------------------------------------------------------------
+ * SwiGLU: z [M, 2*d_ff] (gate || up) -> out [M, d_ff].
+ * fwd replaces SwigluForward RuntimeOp::pack_args (src/kernels/swiglu.rs:151-173):
+ *   (z, out, M, d_ff); bwd replaces pack_backward_args (:179-207):
+ *   (grad, z, dz, M, d_ff).
+ * ------------------------------------------------------------------------ */
+int teeny_swiglu_fwd(const void* z, void* out, int M, int d_ff, int dtype, hipStream_t stream);
+int teeny_swiglu_bwd(const void* grad, const void* z, void* dz, int M, int d_ff, int dtype,
+                     hipStream_t stream);
+
+/* --------------------------------------------------------------------------
+ * Token embedding gather: out[s, :] = weight[ids[s], :].
+ * Replaces TokenEmbedRuntimeOp::pack_args (src/layers/embedding.rs:56-72):
+ *   (ids, weight, out, seq_len, d_model).  ids_dtype TEENY_F32 (the
+ *   reference's encoding, src/kernels/token_embed.rs:32) or TEENY_I32; an id
+ *   outside [0, vocab_size) gives a zero row.
+ * ------------------------------------------------------------------------ */
+int teeny_token_embed_fwd(const void* ids, const void* weight, void* out, int seq_len,
+                          int d_model, int vocab_size, int ids_dtype, int dtype,
+                          hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TEENY_HIP_H */

@@ -1,0 +1,509 @@
+// C-ABI host library: validates arguments, picks the kernel instance and
+// launches it with hipModuleLaunchKernel on the caller's stream.
+//
+// The gfx950 code objects (one per kernel source file, built with
+// `hipcc --genco`) are embedded in this shared library and loaded with
+// hipModuleLoadData once per device, on first use or from teeny_init().
+// This plays the role of the reference's compile-to-PTX + load_program +
+// device.launch sequence (tests/kernel_execution.rs:81-99), without any
+// runtime compilation.
+#include "teeny_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+// ---------------------------------------------------------------------------
+// Embedded code objects (symbols defined by the generated co_blob.S)
+// ---------------------------------------------------------------------------
+#define TEENY_CO_LIST(X) \
+  X(transpose)           \
+  X(rope)                \
+  X(norm)                \
+  X(swiglu)              \
+  X(embed)               \
+  X(fa2_f32)             \
+  X(fa2_fwd_bf16)        \
+  X(fa2_bwd_bf16)
+
+#define TEENY_CO_DECL(n) \
+  extern "C" const unsigned char teeny_co_##n[]; \
+  extern "C" const unsigned char teeny_co_##n##_end[];
+TEENY_CO_LIST(TEENY_CO_DECL)
+
+namespace {
+
+struct CodeObject {
+  const char* name;
+  const unsigned char* begin;
+  const unsigned char* end;
+};
+
+#define TEENY_CO_ENTRY(n) {#n, teeny_co_##n, teeny_co_##n##_end},
+const CodeObject kCodeObjects[] = {TEENY_CO_LIST(TEENY_CO_ENTRY)};
+constexpr int kNumCodeObjects = sizeof(kCodeObjects) / sizeof(kCodeObjects[0]);
+constexpr int kMaxDevices = 64;
+
+struct DeviceState {
+  hipModule_t mods[kNumCodeObjects] = {};
+  std::unordered_map<std::string, hipFunction_t> fns;
+};
+
+std::mutex g_mu;
+DeviceState* g_dev[kMaxDevices] = {};
+thread_local int g_last_hip = 0;
+
+int hip_fail(hipError_t e) {
+  g_last_hip = (int)e;
+  return TEENY_ERR_HIP;
+}
+
+// Loads every code object on the current device (caller holds g_mu).
+int load_device_locked(int dev, DeviceState** out) {
+  if (g_dev[dev]) {
+    *out = g_dev[dev];
+    return TEENY_OK;
+  }
+  DeviceState* st = new DeviceState();
+  for (int i = 0; i < kNumCodeObjects; ++i) {
+    hipError_t e = hipModuleLoadData(&st->mods[i], kCodeObjects[i].begin);
+    if (e != hipSuccess) {
+      g_last_hip = (int)e;
+      for (int j = 0; j < i; ++j) (void)hipModuleUnload(st->mods[j]);
+      delete st;
+      return TEENY_ERR_MODULE;
+    }
+  }
+  g_dev[dev] = st;
+  *out = st;
+  return TEENY_OK;
+}
+
+int get_function(const char* name, hipFunction_t* fn) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e);
+  if (dev < 0 || dev >= kMaxDevices) return TEENY_ERR_HIP;
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState* st = nullptr;
+  int rc = load_device_locked(dev, &st);
+  if (rc) return rc;
+  auto it = st->fns.find(name);
+  if (it != st->fns.end()) {
+    *fn = it->second;
+    return TEENY_OK;
+  }
+  for (int i = 0; i < kNumCodeObjects; ++i) {
+    hipFunction_t f = nullptr;
+    if (hipModuleGetFunction(&f, st->mods[i], name) == hipSuccess && f) {
+      st->fns.emplace(name, f);
+      *fn = f;
+      return TEENY_OK;
+    }
+  }
+  (void)hipGetLastError();  // clear the lookup misses
+  return TEENY_ERR_MODULE;
+}
+
+int launch(const char* name, dim3 grid, dim3 block, unsigned shmem, hipStream_t stream,
+           void** args) {
+  if (grid.x == 0 || grid.y == 0 || grid.z == 0) return TEENY_OK;  // nothing to do
+  hipFunction_t f = nullptr;
+  int rc = get_function(name, &f);
+  if (rc) return rc;
+  hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
+                                       shmem, stream, args, nullptr);
+  if (e != hipSuccess) return hip_fail(e);
+  return TEENY_OK;
+}
+
+const char* dtype_tag(int dtype) { return dtype == TEENY_BF16 ? "bf16" : "f32"; }
+size_t dtype_size(int dtype) { return dtype == TEENY_BF16 ? 2 : 4; }
+bool dtype_ok(int dtype) { return dtype == TEENY_F32 || dtype == TEENY_BF16; }
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+constexpr long kMaxElems = 1L << 31;  // kernels index rows with 32-bit ints where safe
+
+// ---------------------------------------------------------------------------
+// Flash attention
+// ---------------------------------------------------------------------------
+bool fa2_head_dim_ok(int head_dim, int dtype) {
+  if (dtype == TEENY_BF16) return head_dim == 64 || head_dim == 128;
+  return head_dim == 8 || head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128;
+}
+
+int fa2_check(const void* q, const void* k, const void* v, int n_ctx_q, int n_ctx_k, int batch,
+              int hq, int hkv, int head_dim, int dtype) {
+  if (!q || !k || !v) return TEENY_ERR_NULL_POINTER;
+  if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
+  if (n_ctx_q <= 0 || n_ctx_k <= 0 || batch <= 0 || hq <= 0 || hkv <= 0 || hq % hkv != 0)
+    return TEENY_ERR_INVALID_SHAPE;
+  if ((long)batch * hq * n_ctx_q * head_dim >= kMaxElems ||
+      (long)batch * hkv * n_ctx_k * head_dim >= kMaxElems)
+    return TEENY_ERR_INVALID_SHAPE;
+  if (!fa2_head_dim_ok(head_dim, dtype)) return TEENY_ERR_UNSUPPORTED;
+  return TEENY_OK;
+}
+
+int fa2_fwd(bool causal, const void* q, const void* k, const void* v, void* o, float* l,
+            int n_ctx_q, int n_ctx_k, float scale, float neg_inf, int batch, int hq, int hkv,
+            int head_dim, int dtype, hipStream_t stream) {
+  int rc = fa2_check(q, k, v, n_ctx_q, n_ctx_k, batch, hq, hkv, head_dim, dtype);
+  if (rc) return rc;
+  if (!o || !l) return TEENY_ERR_NULL_POINTER;
+  if (!(std::isinf(neg_inf) && neg_inf < 0)) return TEENY_ERR_INVALID_VALUE;
+  if (!std::isfinite(scale)) return TEENY_ERR_INVALID_VALUE;
+  char name[64];
+  const char* cz = causal ? "c" : "n";
+  if (dtype == TEENY_BF16) {
+    int nmb = (n_ctx_q + 127) / 128;
+    long total = (long)nmb * batch * hq;
+    if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
+    int tot = (int)total;
+    snprintf(name, sizeof name, "teeny_fa2_fwd_bf16_d%d_%s", head_dim, cz);
+    void* args[] = {&q, &k, &v, &o, &l, &n_ctx_q, &n_ctx_k, &scale, &hq, &hkv, &nmb, &tot};
+    return launch(name, dim3(tot), dim3(256), 0, stream, args);
+  }
+  snprintf(name, sizeof name, "teeny_fa2_fwd_f32_d%d_%s", head_dim, cz);
+  void* args[] = {&q, &k, &v, &o, &l, &n_ctx_q, &n_ctx_k, &scale, &hq, &hkv};
+  return launch(name, dim3((n_ctx_q + 63) / 64, batch * hq), dim3(64), 0, stream, args);
+}
+
+size_t fa2_bwd_ws(int n_ctx_q, int batch, int hq, int head_dim, int dtype) {
+  size_t rows = (size_t)batch * hq * n_ctx_q;
+  size_t ws = align256(rows * sizeof(float));
+  if (dtype == TEENY_BF16) ws += align256(rows * head_dim * sizeof(float));
+  return ws;
+}
+
+int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void* o,
+            const void* dout, const float* l, void* dq, void* dk, void* dv, int n_ctx_q,
+            int n_ctx_k, float scale, int batch, int hq, int hkv, int head_dim, int dtype,
+            void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  int rc = fa2_check(q, k, v, n_ctx_q, n_ctx_k, batch, hq, hkv, head_dim, dtype);
+  if (rc) return rc;
+  if (!o || !dout || !l || !dq || !dk || !dv) return TEENY_ERR_NULL_POINTER;
+  if (!std::isfinite(scale)) return TEENY_ERR_INVALID_VALUE;
+  if (!workspace || workspace_bytes < fa2_bwd_ws(n_ctx_q, batch, hq, head_dim, dtype))
+    return TEENY_ERR_WORKSPACE;
+  const long rows = (long)batch * hq * n_ctx_q;
+  float* delta = (float*)workspace;
+  const char* cz = causal ? "c" : "n";
+  char name[64];
+  if (dtype == TEENY_BF16) {
+    float* dq_acc = (float*)((char*)workspace + align256(rows * sizeof(float)));
+    const int rows_per_block = 256 / (head_dim / 8);
+    snprintf(name, sizeof name, "teeny_fa2_bwd_pre_bf16_d%d", head_dim);
+    void* a0[] = {&o, &dout, &delta, &dq_acc, (void*)&rows};
+    rc = launch(name, dim3((unsigned)((rows + rows_per_block - 1) / rows_per_block)), dim3(256),
+                0, stream, a0);
+    if (rc) return rc;
+    int nnb = (n_ctx_k + 127) / 128;
+    long total = (long)nnb * batch * hkv;
+    if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
+    int tot = (int)total;
+    snprintf(name, sizeof name, "teeny_fa2_bwd_bf16_d%d_%s", head_dim, cz);
+    void* a1[] = {&q,       &k,       &v,     &dout, &l,     &delta, &dq_acc, &dk,  &dv,
+                  &n_ctx_q, &n_ctx_k, &scale, &hq,   &hkv,   &nnb,   &tot};
+    rc = launch(name, dim3(tot), dim3(256), 0, stream, a1);
+    if (rc) return rc;
+    long n8 = rows * head_dim / 8;
+    void* a2[] = {&dq_acc, &dq, &scale, &n8};
+    return launch("teeny_fa2_bwd_dq_convert_bf16", dim3((unsigned)((n8 + 255) / 256)), dim3(256),
+                  0, stream, a2);
+  }
+  snprintf(name, sizeof name, "teeny_fa2_bwd_pre_f32_d%d", head_dim);
+  void* a0[] = {&o, &dout, &delta, (void*)&rows};
+  rc = launch(name, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream, a0);
+  if (rc) return rc;
+  snprintf(name, sizeof name, "teeny_fa2_bwd_dq_f32_d%d_%s", head_dim, cz);
+  void* a1[] = {&q, &k, &v, &dout, &l, &delta, &dq, &n_ctx_q, &n_ctx_k, &scale, &hq, &hkv};
+  rc = launch(name, dim3((n_ctx_q + 63) / 64, batch * hq), dim3(64), 0, stream, a1);
+  if (rc) return rc;
+  snprintf(name, sizeof name, "teeny_fa2_bwd_dkdv_f32_d%d_%s", head_dim, cz);
+  void* a2[] = {&q,  &k,  &v,       &dout,    &l,     &delta, &dk,
+                &dv, &n_ctx_q, &n_ctx_k, &scale, &hq,    &hkv};
+  return launch(name, dim3((n_ctx_k + 63) / 64, batch * hkv), dim3(64), 0, stream, a2);
+}
+
+// ---------------------------------------------------------------------------
+// Row-wise norms
+// ---------------------------------------------------------------------------
+// Picks (VEC, CH) so one wavefront covers a row of N elements.
+bool norm_shape(int N, int dtype, int* vec, int* ch) {
+  const int v16 = dtype == TEENY_BF16 ? 8 : 4;
+  int v = (N % v16 == 0) ? v16 : 1;
+  int need = (N + 64 * v - 1) / (64 * v);
+  int c = 1;
+  while (c < need) c <<= 1;
+  if (c > 16) return false;
+  *vec = v;
+  *ch = c;
+  return true;
+}
+
+constexpr int kNormBwdMaxParts = 256;
+
+int norm_bwd_parts(int M) {
+  int p = (M + 3) / 4;
+  return p < kNormBwdMaxParts ? p : kNormBwdMaxParts;
+}
+
+}  // namespace
+
+// ===========================================================================
+// Exported entry points
+// ===========================================================================
+extern "C" {
+
+int teeny_abi_version(void) { return TEENY_ABI_VERSION; }
+
+int teeny_last_hip_error(void) { return g_last_hip; }
+
+const char* teeny_strerror(int code) {
+  switch (code) {
+    case TEENY_OK: return "ok";
+    case TEENY_ERR_NULL_POINTER: return "null pointer";
+    case TEENY_ERR_INVALID_SHAPE: return "invalid shape";
+    case TEENY_ERR_UNSUPPORTED: return "unsupported dtype or head_dim";
+    case TEENY_ERR_WORKSPACE: return "workspace missing or too small";
+    case TEENY_ERR_HIP: return "HIP runtime error";
+    case TEENY_ERR_MODULE: return "code object or kernel could not be loaded";
+    case TEENY_ERR_INVALID_VALUE: return "invalid scalar argument";
+    default: return "unknown error";
+  }
+}
+
+int teeny_init(void) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e);
+  if (dev < 0 || dev >= kMaxDevices) return TEENY_ERR_HIP;
+  std::lock_guard<std::mutex> lk(g_mu);
+  DeviceState* st = nullptr;
+  return load_device_locked(dev, &st);
+}
+
+int teeny_causal_flash_attn2_fwd(const void* q, const void* k, const void* v, void* o, float* l,
+                                 int n_ctx_q, int n_ctx_k, float softmax_scale, float neg_inf,
+                                 int batch, int n_heads_q, int n_heads_kv, int head_dim,
+                                 int dtype, hipStream_t stream) {
+  return fa2_fwd(true, q, k, v, o, l, n_ctx_q, n_ctx_k, softmax_scale, neg_inf, batch, n_heads_q,
+                 n_heads_kv, head_dim, dtype, stream);
+}
+
+int teeny_flash_attn2_fwd(const void* q, const void* k, const void* v, void* o, float* l,
+                          int n_ctx_q, int n_ctx_k, float softmax_scale, float neg_inf,
+                          int batch, int n_heads_q, int n_heads_kv, int head_dim, int dtype,
+                          hipStream_t stream) {
+  return fa2_fwd(false, q, k, v, o, l, n_ctx_q, n_ctx_k, softmax_scale, neg_inf, batch,
+                 n_heads_q, n_heads_kv, head_dim, dtype, stream);
+}
+
+int teeny_causal_flash_attn2_bwd(const void* q, const void* k, const void* v, const void* o,
+                                 const void* dout, const float* l, void* dq, void* dk, void* dv,
+                                 int n_ctx_q, int n_ctx_k, float softmax_scale, int batch,
+                                 int n_heads_q, int n_heads_kv, int head_dim, int dtype,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return fa2_bwd(true, q, k, v, o, dout, l, dq, dk, dv, n_ctx_q, n_ctx_k, softmax_scale, batch,
+                 n_heads_q, n_heads_kv, head_dim, dtype, workspace, workspace_bytes, stream);
+}
+
+int teeny_flash_attn2_bwd(const void* q, const void* k, const void* v, const void* o,
+                          const void* dout, const float* l, void* dq, void* dk, void* dv,
+                          int n_ctx_q, int n_ctx_k, float softmax_scale, int batch, int n_heads_q,
+                          int n_heads_kv, int head_dim, int dtype, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream) {
+  return fa2_bwd(false, q, k, v, o, dout, l, dq, dk, dv, n_ctx_q, n_ctx_k, softmax_scale, batch,
+                 n_heads_q, n_heads_kv, head_dim, dtype, workspace, workspace_bytes, stream);
+}
+
+size_t teeny_flash_attn2_bwd_workspace_bytes(int n_ctx_q, int batch, int n_heads_q, int head_dim,
+                                             int dtype) {
+  if (n_ctx_q <= 0 || batch <= 0 || n_heads_q <= 0 || head_dim <= 0) return 0;
+  return fa2_bwd_ws(n_ctx_q, batch, n_heads_q, head_dim, dtype);
+}
+
+static int rope_impl(const void* x, void* y, int n_ctx, float ln_base, int bh, int head_dim,
+                     int dtype, int backward, hipStream_t stream) {
+  if (!x || !y) return TEENY_ERR_NULL_POINTER;
+  if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
+  if (n_ctx <= 0 || bh <= 0 || head_dim <= 0 || (long)bh * n_ctx * head_dim >= kMaxElems)
+    return TEENY_ERR_INVALID_SHAPE;
+  const int vn = dtype == TEENY_BF16 ? 8 : 4;
+  if (head_dim % vn != 0) return TEENY_ERR_UNSUPPORTED;
+  if (!std::isfinite(ln_base)) return TEENY_ERR_INVALID_VALUE;
+  char name[32];
+  snprintf(name, sizeof name, "teeny_rope_%s", dtype_tag(dtype));
+  void* args[] = {&x, &y, &bh, &n_ctx, &head_dim, &ln_base, &backward};
+  unsigned shmem = 16u * (unsigned)(head_dim / 2) * 8u;
+  return launch(name, dim3((n_ctx + 15) / 16, (bh + 15) / 16), dim3(256), shmem, stream, args);
+}
+
+int teeny_rope_fwd(const void* x, void* y, int n_ctx, float ln_rope_base, int bh, int head_dim,
+                   int dtype, hipStream_t stream) {
+  return rope_impl(x, y, n_ctx, ln_rope_base, bh, head_dim, dtype, 0, stream);
+}
+
+int teeny_rope_bwd(const void* dy, void* dx, int n_ctx, float ln_rope_base, int bh, int head_dim,
+                   int dtype, hipStream_t stream) {
+  return rope_impl(dy, dx, n_ctx, ln_rope_base, bh, head_dim, dtype, 1, stream);
+}
+
+static int transpose_impl(const void* src, void* dst, int seq, int heads, int batch,
+                          int head_dim, int dtype, int merge, hipStream_t stream) {
+  if (!src || !dst) return TEENY_ERR_NULL_POINTER;
+  if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
+  if (seq <= 0 || heads <= 0 || batch <= 0 || head_dim <= 0 || batch * heads > 65535 ||
+      (long)batch * heads * seq * head_dim >= kMaxElems)
+    return TEENY_ERR_INVALID_SHAPE;
+  if (src == dst) return TEENY_ERR_INVALID_VALUE;  // not an in-place permutation
+  int row_bytes = head_dim * (int)dtype_size(dtype);
+  if (row_bytes % 4 != 0) return TEENY_ERR_UNSUPPORTED;
+  const bool v16 = row_bytes % 16 == 0;
+  const int vb = v16 ? 16 : 4;
+  long per_slice = (long)seq * (row_bytes / vb);
+  unsigned gx = (unsigned)((per_slice + 1023) / 1024);
+  void* args[] = {&src, &dst, &seq, &heads, &row_bytes, &merge};
+  return launch(v16 ? "teeny_transpose_heads_v16" : "teeny_transpose_heads_v4",
+                dim3(gx, batch * heads), dim3(256), 0, stream, args);
+}
+
+int teeny_transpose_heads(const void* src, void* dst, int seq_len, int n_heads, int batch,
+                          int head_dim, int dtype, hipStream_t stream) {
+  return transpose_impl(src, dst, seq_len, n_heads, batch, head_dim, dtype, 0, stream);
+}
+
+int teeny_merge_heads(const void* src, void* dst, int seq_len, int n_heads, int batch,
+                      int head_dim, int dtype, hipStream_t stream) {
+  return transpose_impl(src, dst, seq_len, n_heads, batch, head_dim, dtype, 1, stream);
+}
+
+static int norm_fwd_impl(const void* x, const void* res, void* y, void* h, float* rstd,
+                         const void* w, int M, int N, float eps, int dtype, hipStream_t stream) {
+  if (!x || !y || !w) return TEENY_ERR_NULL_POINTER;
+  if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
+  if (M <= 0 || N <= 0 || (long)M * N >= kMaxElems) return TEENY_ERR_INVALID_SHAPE;
+  if (!(eps >= 0.0f) || !std::isfinite(eps)) return TEENY_ERR_INVALID_VALUE;
+  int vec, ch;
+  if (!norm_shape(N, dtype, &vec, &ch)) return TEENY_ERR_UNSUPPORTED;
+  char name[64];
+  snprintf(name, sizeof name, "teeny_rmsnorm_fwd_%s_v%d_c%d", dtype_tag(dtype), vec, ch);
+  void* args[] = {&x, &res, &y, &h, &rstd, &w, &M, &N, &eps};
+  return launch(name, dim3((M + 3) / 4), dim3(256), 0, stream, args);
+}
+
+int teeny_fused_add_rmsnorm_fwd(const void* x, const void* residual, void* y, void* h,
+                                float* rstd, const void* weight, int M, int N, float eps,
+                                int dtype, hipStream_t stream) {
+  if (!residual || !h || !rstd) return TEENY_ERR_NULL_POINTER;
+  return norm_fwd_impl(x, residual, y, h, rstd, weight, M, N, eps, dtype, stream);
+}
+
+int teeny_rmsnorm_fwd(const void* x, void* y, float* rstd, const void* weight, int M, int N,
+                      float eps, int dtype, hipStream_t stream) {
+  return norm_fwd_impl(x, nullptr, y, nullptr, rstd, weight, M, N, eps, dtype, stream);
+}
+
+size_t teeny_fused_add_rmsnorm_bwd_workspace_bytes(int M, int N) {
+  if (M <= 0 || N <= 0) return 0;
+  return align256((size_t)norm_bwd_parts(M) * N * sizeof(float));
+}
+
+static int norm_bwd_impl(bool ref_formula, const void* dy, const void* h, void* dx,
+                         void* dresidual, void* dweight, const void* weight, const float* rstd,
+                         int M, int N, int dtype, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream) {
+  if (!dy || !h || !dx || !dweight || !weight || !rstd) return TEENY_ERR_NULL_POINTER;
+  if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
+  if (M <= 0 || N <= 0 || (long)M * N >= kMaxElems) return TEENY_ERR_INVALID_SHAPE;
+  int vec, ch;
+  if (!norm_shape(N, dtype, &vec, &ch)) return TEENY_ERR_UNSUPPORTED;
+  if (!workspace || workspace_bytes < teeny_fused_add_rmsnorm_bwd_workspace_bytes(M, N))
+    return TEENY_ERR_WORKSPACE;
+  int parts = norm_bwd_parts(M);
+  float* part = (float*)workspace;
+  char name[64];
+  snprintf(name, sizeof name, "teeny_%s_bwd_%s_v%d_c%d", ref_formula ? "addnorm" : "rmsnorm",
+           dtype_tag(dtype), vec, ch);
+  void* a0[] = {&dy, &h, &dx, &dresidual, &part, &weight, &rstd, &M, &N};
+  int rc = launch(name, dim3(parts), dim3(256), 0, stream, a0);
+  if (rc) return rc;
+  snprintf(name, sizeof name, "teeny_rmsnorm_dw_reduce_%s", dtype_tag(dtype));
+  void* a1[] = {&part, &dweight, &parts, &N};
+  return launch(name, dim3((N + 255) / 256), dim3(256), 0, stream, a1);
+}
+
+int teeny_fused_add_rmsnorm_bwd(const void* dy, const void* h, void* dx, void* dresidual,
+                                void* dweight, const void* weight, const float* rstd, int M,
+                                int N, int dtype, void* workspace, size_t workspace_bytes,
+                                hipStream_t stream) {
+  return norm_bwd_impl(true, dy, h, dx, dresidual, dweight, weight, rstd, M, N, dtype, workspace,
+                       workspace_bytes, stream);
+}
+
+int teeny_rmsnorm_bwd(const void* dy, const void* x, void* dx, void* dweight, const void* weight,
+                      const float* rstd, int M, int N, int dtype, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream) {
+  return norm_bwd_impl(false, dy, x, dx, nullptr, dweight, weight, rstd, M, N, dtype, workspace,
+                       workspace_bytes, stream);
+}
+
+static int swiglu_impl(bool bwd, const void* grad, const void* z, void* out, int M, int d_ff,
+                       int dtype, hipStream_t stream) {
+  if (!z || !out || (bwd && !grad)) return TEENY_ERR_NULL_POINTER;
+  if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
+  if (M <= 0 || d_ff <= 0 || M > 65535 * 64 || (long)M * 2 * d_ff >= kMaxElems)
+    return TEENY_ERR_INVALID_SHAPE;
+  const int v16 = dtype == TEENY_BF16 ? 8 : 4;
+  const int vec = d_ff % v16 == 0 ? v16 : 1;
+  if (M > 65535) return TEENY_ERR_INVALID_SHAPE;
+  char name[48];
+  snprintf(name, sizeof name, "teeny_swiglu_%s_%s_v%d", bwd ? "bwd" : "fwd", dtype_tag(dtype),
+           vec);
+  dim3 grid((d_ff / vec + 255) / 256, M);
+  if (bwd) {
+    void* args[] = {&grad, &z, &out, &M, &d_ff};
+    return launch(name, grid, dim3(256), 0, stream, args);
+  }
+  void* args[] = {&z, &out, &M, &d_ff};
+  return launch(name, grid, dim3(256), 0, stream, args);
+}
+
+int teeny_swiglu_fwd(const void* z, void* out, int M, int d_ff, int dtype, hipStream_t stream) {
+  return swiglu_impl(false, nullptr, z, out, M, d_ff, dtype, stream);
+}
+
+int teeny_swiglu_bwd(const void* grad, const void* z, void* dz, int M, int d_ff, int dtype,
+                     hipStream_t stream) {
+  return swiglu_impl(true, grad, z, dz, M, d_ff, dtype, stream);
+}
+
+int teeny_token_embed_fwd(const void* ids, const void* weight, void* out, int seq_len,
+                          int d_model, int vocab_size, int ids_dtype, int dtype,
+                          hipStream_t stream) {
+  if (!ids || !weight || !out) return TEENY_ERR_NULL_POINTER;
+  if (!dtype_ok(dtype) || (ids_dtype != TEENY_F32 && ids_dtype != TEENY_I32))
+    return TEENY_ERR_UNSUPPORTED;
+  if (seq_len <= 0 || d_model <= 0 || vocab_size <= 0 || seq_len > 65535 ||
+      (long)vocab_size * d_model >= kMaxElems * 2)
+    return TEENY_ERR_INVALID_SHAPE;
+  int row_bytes = d_model * (int)dtype_size(dtype);
+  if (row_bytes % 4 != 0) return TEENY_ERR_UNSUPPORTED;
+  const bool v16 = row_bytes % 16 == 0;
+  const int vb = v16 ? 16 : 4;
+  char name[48];
+  snprintf(name, sizeof name, "teeny_embed_%sids_v%d", ids_dtype == TEENY_I32 ? "i32" : "f32",
+           vb);
+  void* args[] = {&ids, &weight, &out, &row_bytes, &vocab_size};
+  dim3 grid((row_bytes / vb + 255) / 256, seq_len);
+  return launch(name, grid, dim3(256), 0, stream, args);
+}
+
+}  // extern "C"

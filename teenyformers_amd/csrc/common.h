@@ -1,0 +1,96 @@
+// Shared device-side helpers for the gfx950 (CDNA4) kernels.
+//
+// Every kernel is `extern "C" __global__` so the host library can look it up
+// by name in the code object with hipModuleGetFunction.  Storage types are
+// fp32 (`float`) and bf16 (`__bf16`, bit-compatible with the IEEE upper half
+// of an fp32); arithmetic is always fp32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define DEVI __device__ __forceinline__
+
+// MI355X: 8 accelerator complex dies (XCDs), each with its own L2.  The
+// dispatcher hands consecutive workgroup ids to XCDs round-robin.
+#define TEENY_NUM_XCD 8
+
+DEVI float bf2f(bf16 x) { return (float)x; }
+DEVI bf16 f2bf(float x) { return (bf16)x; }  // round to nearest even
+
+DEVI uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2 v = __builtin_convertvector((f32x2){lo, hi}, bf16x2);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Low / high bf16 of a packed pair, widened to fp32.
+DEVI float bf16lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+DEVI float bf16hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+// Generic element load/store with fp32 arithmetic.
+template <typename T> DEVI float ld(const T* p) { return (float)*p; }
+template <typename T> DEVI void st(T* p, float v) { *p = (T)v; }
+
+// 16-byte vector of storage elements (8 x bf16 or 4 x fp32) converted to fp32.
+template <typename T> struct Vec16;
+template <> struct Vec16<float> {
+  static constexpr int N = 4;
+  DEVI static void load(const float* p, float* out) {
+    f32x4 v = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = v[i];
+  }
+  DEVI static void store(float* p, const float* in) {
+    f32x4 v = {in[0], in[1], in[2], in[3]};
+    *reinterpret_cast<f32x4*>(p) = v;
+  }
+};
+template <> struct Vec16<bf16> {
+  static constexpr int N = 8;
+  DEVI static void load(const bf16* p, float* out) {
+    u32x4 v = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = bf16lo(v[i]);
+      out[2 * i + 1] = bf16hi(v[i]);
+    }
+  }
+  DEVI static void store(bf16* p, const float* in) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(in[2 * i], in[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(p) = v;
+  }
+};
+
+// Wavefront (64-lane) reductions through DPP/permute, all lanes get the result.
+DEVI float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+DEVI float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Remap a linear workgroup id so that consecutive ids in the returned space
+// land on the same XCD (the hardware deals ids round-robin across XCDs).
+// Bijective for any total.
+DEVI int xcd_remap(int id, int total) {
+  int xcd = id % TEENY_NUM_XCD;
+  int local = id / TEENY_NUM_XCD;
+  int q = total / TEENY_NUM_XCD, r = total % TEENY_NUM_XCD;
+  return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}

@@ -1,0 +1,271 @@
+// bf16 flash-attention 2 forward on CDNA4 matrix cores (gfx950).
+//
+// Reference semantics: flash_attn2_causal_fwd (src/kernels/flash_attn2.rs:61-126)
+// and the bidirectional forward (:57-58): O = softmax(scale * Q K^T [+ causal
+// mask k > q]) V per query row, LSE = m + ln(l) in the natural-log,
+// scaled-score domain (:121-122).  The reference is fp32 with one CTA per
+// query row; this kernel keeps bf16 operands with fp32 accumulation and a
+// fp32 online softmax.
+//
+// Tiling (one workgroup = 4 wavefronts = 128 query rows of one (b, h)):
+//   * each wave owns 32 query rows; its Q rows live in registers as the
+//     B operand of v_mfma_f32_32x32x16_bf16;
+//   * K/V advance in tiles of 64 keys, double-buffered in LDS; K is stored
+//     row-major [key][d] (A operand, 16-byte reads), V is transposed on its
+//     way into LDS as Vt[d][key] so the PV product reads it as an A operand;
+//   * S^T = K Q^T puts one query row in each lane (lane % 32) and 16 keys per
+//     lane per 32-key subtile, so the row max / row sum are in-lane plus one
+//     exchange between the two lane halves;
+//   * the fp32 accumulator of S^T, rounded to bf16, is already in the
+//     B-operand layout of O^T += V^T P^T (keys are a summation index, so the
+//     key order inside each 16-key chunk only has to agree between A and B);
+//   * causal: key tiles past the block's last query row are skipped, subtiles
+//     past a wave's last row are skipped, only diagonal tiles are masked;
+//   * GQA: q head h reads kv head h / (Hq / Hkv);
+//   * scheduling: block ids are remapped so one XCD works through whole heads
+//     (K/V stay in that XCD's L2), heaviest causal blocks first.
+// exp is exp2 with log2(e) folded into the scale (v_exp_f32).
+#include "common.h"
+
+namespace {
+
+constexpr int BM = 128;  // query rows per workgroup
+constexpr int BN = 64;   // keys per iteration
+constexpr int KPAD = 8;  // K tile row padding (elements)
+constexpr int VPAD = 4;  // Vt tile row padding (elements)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+DEVI float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+DEVI bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+DEVI f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int D>
+struct FwdSmem {
+  bf16 k[2][BN][D + KPAD];
+  bf16 vt[2][D][BN + VPAD];
+};
+
+template <int D, bool CAUSAL>
+__device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                             const bf16* __restrict__ v, bf16* __restrict__ o,
+                             float* __restrict__ lse, int nq, int nk, float scale, int hq, int hkv,
+                             int num_m_blocks, int total_blocks) {
+  constexpr int DC = D / 16;              // d-chunks of 16 for QK^T
+  constexpr int DT = D / 32;              // d-tiles of 32 for PV
+  constexpr int CPR = D / 8;              // 16-byte chunks per K row
+  constexpr int KCH = BN * CPR / 256;     // K chunks per thread
+  constexpr int VPAIRS = (BN / 4) * CPR;  // (4-key group, 8-d group) pairs
+  __shared__ FwdSmem<D> sm;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+
+  const int id = xcd_remap(blockIdx.x, total_blocks);
+  const int bh = id / num_m_blocks;
+  const int mb = num_m_blocks - 1 - (id - bh * num_m_blocks);
+  const int b = bh / hq, h = bh - b * hq;
+  const long kvh = (long)b * hkv + h / (hq / hkv);
+  const int m0 = mb * BM;
+  const int qrow = m0 + wave * 32 + l32;
+  const int wave_qmax = m0 + wave * 32 + 31;
+
+  const bf16* kb = k + kvh * (long)nk * D;
+  const bf16* vb = v + kvh * (long)nk * D;
+
+  // ---- Q rows -> registers (B operand) -------------------------------------
+  bf16x8 qreg[DC];
+  {
+    const bool ok = qrow < nq;
+    const bf16* qp = q + ((long)bh * nq + (ok ? qrow : 0)) * D + 8 * g;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      u32x4 t = ok ? *reinterpret_cast<const u32x4*>(qp + 16 * c) : u32x4{0, 0, 0, 0};
+      qreg[c] = as_bf16x8(t);
+    }
+  }
+
+  int kend = nk;
+  if (CAUSAL) kend = min(nk, m0 + BM);
+  const int n_iter = (kend + BN - 1) / BN;
+
+  // ---- global -> register staging of one K/V tile --------------------------
+  u32x4 kstage[KCH];
+  u32x4 vstage[4];
+  const int v_dg = tid % CPR, v_kg = tid / CPR;  // valid when tid < VPAIRS
+  auto load_tile = [&](int kbase) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      int c = i * 256 + tid;
+      int row = c / CPR, col = (c % CPR) * 8;
+      int key = kbase + row;
+      kstage[i] = key < nk ? *reinterpret_cast<const u32x4*>(kb + (long)key * D + col)
+                           : u32x4{0, 0, 0, 0};
+    }
+    if (tid < VPAIRS) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        int key = kbase + 4 * v_kg + r;
+        vstage[r] = key < nk ? *reinterpret_cast<const u32x4*>(vb + (long)key * D + 8 * v_dg)
+                             : u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      int c = i * 256 + tid;
+      int row = c / CPR, col = (c % CPR) * 8;
+      *reinterpret_cast<u32x4*>(&sm.k[buf][row][col]) = kstage[i];
+    }
+    if (tid < VPAIRS) {
+      // 4 keys x 8 d (row-major in vstage) -> 8 d-rows x 4 keys in Vt.
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // d = 8*dg + 2j (low halves) and 8*dg + 2j + 1 (high halves)
+        uint32_t k01_lo = __builtin_amdgcn_perm(vstage[1][j], vstage[0][j], 0x05040100u);
+        uint32_t k23_lo = __builtin_amdgcn_perm(vstage[3][j], vstage[2][j], 0x05040100u);
+        uint32_t k01_hi = __builtin_amdgcn_perm(vstage[1][j], vstage[0][j], 0x07060302u);
+        uint32_t k23_hi = __builtin_amdgcn_perm(vstage[3][j], vstage[2][j], 0x07060302u);
+        *reinterpret_cast<u32x2*>(&sm.vt[buf][8 * v_dg + 2 * j][4 * v_kg]) = u32x2{k01_lo, k23_lo};
+        *reinterpret_cast<u32x2*>(&sm.vt[buf][8 * v_dg + 2 * j + 1][4 * v_kg]) =
+            u32x2{k01_hi, k23_hi};
+      }
+    }
+  };
+
+  // ---- running state ---------------------------------------------------------
+  f32x16 acc_o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) acc_o[t] = f32x16{};
+  float m_run = -INFINITY;  // running max, log2 domain
+  float l_run = 0.0f;       // this lane's partial row sum (its 16 of every 32 keys)
+  const float sl2 = scale * kLog2e;
+
+  if (n_iter > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < n_iter; ++it) {
+    const int cur = it & 1;
+    const int kbase = it * BN;
+    if (it + 1 < n_iter) load_tile(kbase + BN);
+
+    // ---- S^T = K Q^T for the two 32-key subtiles ----
+    f32x16 s[2];
+    bool act[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int key0 = kbase + 32 * kt;
+      act[kt] = key0 < nk && !(CAUSAL && key0 > wave_qmax);
+      s[kt] = f32x16{};
+      if (act[kt]) {
+#pragma unroll
+        for (int c = 0; c < DC; ++c) {
+          u32x4 a = *reinterpret_cast<const u32x4*>(&sm.k[cur][32 * kt + l32][16 * c + 8 * g]);
+          s[kt] = mfma32(as_bf16x8(a), qreg[c], s[kt]);
+        }
+      }
+    }
+
+    // ---- online softmax (log2 domain) ----
+    const bool need_mask = (kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > m0 + wave * 32);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float t = act[kt] ? s[kt][r] * sl2 : -INFINITY;
+        if (need_mask) {
+          int key = kbase + 32 * kt + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (key >= nk || (CAUSAL && key > qrow)) t = -INFINITY;
+        }
+        s[kt][r] = t;
+        mx = fmaxf(mx, t);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = fast_exp2(m_run - m_use);
+    m_run = m_new;
+    float psum = 0.0f;
+    uint32_t pb[2][8];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        float p0 = fast_exp2(s[kt][r] - m_use);
+        float p1 = fast_exp2(s[kt][r + 1] - m_use);
+        psum += p0 + p1;
+        pb[kt][r >> 1] = pack_bf16x2(p0, p1);
+      }
+    }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc_o[t] *= alpha;
+
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      if (!act[kt]) continue;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        bf16x8 bop = as_bf16x8(u32x4{pb[kt][4 * hh], pb[kt][4 * hh + 1], pb[kt][4 * hh + 2],
+                                     pb[kt][4 * hh + 3]});
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          const bf16* vrow = &sm.vt[cur][32 * t + l32][32 * kt + 16 * hh + 4 * g];
+          u32x2 a0 = *reinterpret_cast<const u32x2*>(vrow);
+          u32x2 a1 = *reinterpret_cast<const u32x2*>(vrow + 8);
+          acc_o[t] = mfma32(as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]}), bop, acc_o[t]);
+        }
+      }
+    }
+
+    if (it + 1 < n_iter) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue ----
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (qrow < nq) {
+    const float inv = 1.0f / l_tot;
+    bf16* orow = o + ((long)bh * nq + qrow) * D;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int d = 32 * t + 8 * j + 4 * g;
+        u32x2 w = {pack_bf16x2(acc_o[t][4 * j] * inv, acc_o[t][4 * j + 1] * inv),
+                   pack_bf16x2(acc_o[t][4 * j + 2] * inv, acc_o[t][4 * j + 3] * inv)};
+        *reinterpret_cast<u32x2*>(orow + d) = w;
+      }
+    }
+    if (g == 0) lse[(long)bh * nq + qrow] = (m_run + __log2f(l_tot)) * kLn2;
+  }
+}
+
+}  // namespace
+
+#define TEENY_FA2_FWD_BF16_INST(D)                                                               \
+  extern "C" __global__ __launch_bounds__(256) void teeny_fa2_fwd_bf16_d##D##_c(               \
+      const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,            \
+      float scale, int hq, int hkv, int nmb, int total) {                                        \
+    fa2_fwd_bf16<D, true>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);                    \
+  }                                                                                              \
+  extern "C" __global__ __launch_bounds__(256) void teeny_fa2_fwd_bf16_d##D##_n(               \
+      const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,            \
+      float scale, int hq, int hkv, int nmb, int total) {                                        \
+    fa2_fwd_bf16<D, false>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);                   \
+  }
+
+TEENY_FA2_FWD_BF16_INST(64)
+TEENY_FA2_FWD_BF16_INST(128)

@@ -1,0 +1,326 @@
+"""Functional API over torch tensors; every op runs the HIP kernels through
+the C ABI (include/teeny_hip.h).  torch only supplies device memory and the
+current stream.
+
+Shapes follow the reference with the batch split out:
+  attention tensors  [B, H, S, D]   (reference [BH, S, D], flash_attn2.rs:23)
+  activations        [..., N]       (rows x columns)
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from ._lib import TEENY_BF16, TEENY_F32, TEENY_I32, call
+
+_DTYPES = {torch.float32: TEENY_F32, torch.bfloat16: TEENY_BF16}
+
+
+def _code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; expected float32 or bfloat16") from None
+
+
+def _dev(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("teenyformers_amd ops take device tensors (no CPU fallback)")
+        if not t.is_contiguous():
+            raise ValueError("teenyformers_amd ops take contiguous tensors")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _as4(x: torch.Tensor) -> torch.Tensor:
+    """[BH, S, D] -> [1, BH, S, D]; [B, H, S, D] unchanged."""
+    if x.dim() == 3:
+        return x.unsqueeze(0)
+    if x.dim() != 4:
+        raise ValueError(f"attention tensors are [B, H, S, D] or [BH, S, D], got {tuple(x.shape)}")
+    return x
+
+
+# ---------------------------------------------------------------------------
+# Flash attention 2
+# ---------------------------------------------------------------------------
+
+def flash_attn2_fwd(q, k, v, softmax_scale: float | None = None, causal: bool = True,
+                    out: torch.Tensor | None = None, lse: torch.Tensor | None = None):
+    """O = softmax(scale Q K^T [+ causal]) V and LSE (fp32, natural log).
+
+    q [B, Hq, Sq, D], k/v [B, Hkv, Sk, D] (or [BH, S, D]).  Returns (o, lse)
+    with lse [B, Hq, Sq].
+    """
+    q4, k4, v4 = _as4(q), _as4(k), _as4(v)
+    _dev(q4, k4, v4)
+    B, Hq, Sq, D = q4.shape
+    Hkv, Sk = k4.shape[1], k4.shape[2]
+    if k4.shape != v4.shape or k4.shape[0] != B or k4.shape[3] != D:
+        raise ValueError("k and v must be [B, Hkv, Sk, D] matching q")
+    if q4.dtype != k4.dtype or q4.dtype != v4.dtype:
+        raise TypeError("q, k, v must share a dtype")
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    if out is None:
+        out = torch.empty_like(q)
+    if lse is None:
+        lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device)
+    _dev(out, lse)
+    fn = "teeny_causal_flash_attn2_fwd" if causal else "teeny_flash_attn2_fwd"
+    call(fn, _p(q4), _p(k4), _p(v4), _p(out), _p(lse), Sq, Sk, scale, float("-inf"),
+         B, Hq, Hkv, D, _code(q4), _stream())
+    return out, lse
+
+
+def flash_attn2_bwd_workspace_bytes(q: torch.Tensor) -> int:
+    q4 = _as4(q)
+    B, Hq, Sq, D = q4.shape
+    return _lib.lib().teeny_flash_attn2_bwd_workspace_bytes(Sq, B, Hq, D, _code(q4))
+
+
+def flash_attn2_bwd(q, k, v, o, lse, do, softmax_scale: float | None = None, causal: bool = True,
+                    workspace: torch.Tensor | None = None, dq=None, dk=None, dv=None):
+    """Gradients (dq, dk, dv) of sum(O * dO); dk/dv summed over each GQA group."""
+    q4, k4, v4, o4, do4 = _as4(q), _as4(k), _as4(v), _as4(o), _as4(do)
+    _dev(q4, k4, v4, o4, do4, lse)
+    B, Hq, Sq, D = q4.shape
+    Hkv, Sk = k4.shape[1], k4.shape[2]
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    ws_bytes = flash_attn2_bwd_workspace_bytes(q4)
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    dq = torch.empty_like(q) if dq is None else dq
+    dk = torch.empty_like(k) if dk is None else dk
+    dv = torch.empty_like(v) if dv is None else dv
+    fn = "teeny_causal_flash_attn2_bwd" if causal else "teeny_flash_attn2_bwd"
+    call(fn, _p(q4), _p(k4), _p(v4), _p(o4), _p(do4), _p(lse), _p(dq), _p(dk), _p(dv),
+         Sq, Sk, scale, B, Hq, Hkv, D, _code(q4), _p(workspace), workspace.numel(), _stream())
+    return dq, dk, dv
+
+
+class FlashAttn2Function(torch.autograd.Function):
+    """Autograd wrapper: forward saves (q, k, v, o, lse) like the reference's
+    LSE param cache (flash_attn2.rs:449-457) and backward recomputes P."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, softmax_scale, causal):
+        o, lse = flash_attn2_fwd(q, k, v, softmax_scale, causal)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.scale, ctx.causal = softmax_scale, causal
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = flash_attn2_bwd(q, k, v, o, lse, do.contiguous(), ctx.scale, ctx.causal)
+        return dq, dk, dv, None, None
+
+
+def flash_attn2(q, k, v, softmax_scale=None, causal=True):
+    return FlashAttn2Function.apply(q, k, v, softmax_scale, causal)
+
+
+# ---------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------
+
+def rope(x: torch.Tensor, rope_base: float, backward: bool = False,
+         out: torch.Tensor | None = None) -> torch.Tensor:
+    """Interleaved-pair rotary embedding on x [..., S, D]; position = S index."""
+    _dev(x)
+    S, D = x.shape[-2], x.shape[-1]
+    bh = x.numel() // (S * D)
+    ln_base = float(torch.tensor(rope_base, dtype=torch.float32).log().item())
+    out = torch.empty_like(x) if out is None else out
+    _dev(out)
+    fn = "teeny_rope_bwd" if backward else "teeny_rope_fwd"
+    call(fn, _p(x), _p(out), S, ln_base, bh, D, _code(x), _stream())
+    return out
+
+
+class RopeFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, rope_base):
+        ctx.rope_base = rope_base
+        return rope(x, rope_base)
+
+    @staticmethod
+    def backward(ctx, dy):
+        return rope(dy.contiguous(), ctx.rope_base, backward=True), None
+
+
+# ---------------------------------------------------------------------------
+# Head transposes
+# ---------------------------------------------------------------------------
+
+def transpose_heads(x: torch.Tensor, n_heads: int) -> torch.Tensor:
+    """[B, S, H*Dh] (or [S, H*Dh]) -> [B, H, S, Dh] (or [H, S, Dh])."""
+    _dev(x)
+    squeeze = x.dim() == 2
+    x3 = x.unsqueeze(0) if squeeze else x
+    B, S, HD = x3.shape
+    if HD % n_heads:
+        raise ValueError("last dim must be n_heads * head_dim")
+    Dh = HD // n_heads
+    out = torch.empty((B, n_heads, S, Dh), dtype=x.dtype, device=x.device)
+    call("teeny_transpose_heads", _p(x3), _p(out), S, n_heads, B, Dh, _code(x), _stream())
+    return out[0] if squeeze else out
+
+
+def merge_heads(x: torch.Tensor) -> torch.Tensor:
+    """[B, H, S, Dh] (or [H, S, Dh]) -> [B, S, H*Dh] (or [S, H*Dh])."""
+    _dev(x)
+    squeeze = x.dim() == 3
+    x4 = x.unsqueeze(0) if squeeze else x
+    B, H, S, Dh = x4.shape
+    out = torch.empty((B, S, H * Dh), dtype=x.dtype, device=x.device)
+    call("teeny_merge_heads", _p(x4), _p(out), S, H, B, Dh, _code(x), _stream())
+    return out[0] if squeeze else out
+
+
+class TransposeHeadsFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, n_heads):
+        return transpose_heads(x, n_heads)
+
+    @staticmethod
+    def backward(ctx, dy):
+        return merge_heads(dy.contiguous()), None
+
+
+class MergeHeadsFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        ctx.n_heads = x.shape[-3]
+        return merge_heads(x)
+
+    @staticmethod
+    def backward(ctx, dy):
+        return transpose_heads(dy.contiguous(), ctx.n_heads)
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+
+def _rows(x: torch.Tensor):
+    N = x.shape[-1]
+    return x.numel() // N, N
+
+
+def fused_add_rmsnorm(x, residual, weight, eps: float):
+    """h = x + residual; y = h * rsqrt(mean(h^2) + eps) * weight -> (y, h, rstd)."""
+    _dev(x, residual, weight)
+    M, N = _rows(x)
+    y = torch.empty_like(x)
+    h = torch.empty_like(x)
+    rstd = torch.empty(M, dtype=torch.float32, device=x.device)
+    call("teeny_fused_add_rmsnorm_fwd", _p(x), _p(residual), _p(y), _p(h), _p(rstd), _p(weight),
+         M, N, float(eps), _code(x), _stream())
+    return y, h, rstd
+
+
+def rmsnorm(x, weight, eps: float, want_rstd: bool = True):
+    _dev(x, weight)
+    M, N = _rows(x)
+    y = torch.empty_like(x)
+    rstd = torch.empty(M, dtype=torch.float32, device=x.device) if want_rstd else None
+    call("teeny_rmsnorm_fwd", _p(x), _p(y), _p(rstd), _p(weight), M, N, float(eps), _code(x),
+         _stream())
+    return y, rstd
+
+
+def _norm_ws(M, N, device):
+    return torch.empty(_lib.lib().teeny_fused_add_rmsnorm_bwd_workspace_bytes(M, N),
+                       dtype=torch.uint8, device=device)
+
+
+def fused_add_rmsnorm_bwd(dy, h, weight, rstd, dweight=None, want_dres: bool = True):
+    """The reference's fused backward (fused_add_rmsnorm.rs:128-190) -> (dx, dres, dweight).
+
+    dweight is accumulated into.  Its dx formula is the true gradient only for
+    weight == 1; rmsnorm_bwd is the true gradient for any weight.
+    """
+    _dev(dy, h, weight, rstd)
+    M, N = _rows(dy)
+    dx = torch.empty_like(dy)
+    dres = torch.empty_like(dy) if want_dres else None
+    if dweight is None:
+        dweight = torch.zeros_like(weight)
+    ws = _norm_ws(M, N, dy.device)
+    call("teeny_fused_add_rmsnorm_bwd", _p(dy), _p(h), _p(dx), _p(dres), _p(dweight), _p(weight),
+         _p(rstd), M, N, _code(dy), _p(ws), ws.numel(), _stream())
+    return dx, dres, dweight
+
+
+def rmsnorm_bwd(dy, x, weight, rstd, dweight=None):
+    """True RMSNorm gradient -> (dx, dweight); dweight is accumulated into."""
+    _dev(dy, x, weight, rstd)
+    M, N = _rows(dy)
+    dx = torch.empty_like(dy)
+    if dweight is None:
+        dweight = torch.zeros_like(weight)
+    ws = _norm_ws(M, N, dy.device)
+    call("teeny_rmsnorm_bwd", _p(dy), _p(x), _p(dx), _p(dweight), _p(weight), _p(rstd), M, N,
+         _code(dy), _p(ws), ws.numel(), _stream())
+    return dx, dweight
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU, embedding
+# ---------------------------------------------------------------------------
+
+def swiglu(z: torch.Tensor) -> torch.Tensor:
+    """z [..., 2F] (gate || up) -> silu(gate) * up [..., F]."""
+    _dev(z)
+    M, F2 = _rows(z)
+    out = torch.empty(z.shape[:-1] + (F2 // 2,), dtype=z.dtype, device=z.device)
+    call("teeny_swiglu_fwd", _p(z), _p(out), M, F2 // 2, _code(z), _stream())
+    return out
+
+
+def swiglu_bwd(grad: torch.Tensor, z: torch.Tensor) -> torch.Tensor:
+    _dev(grad, z)
+    M, F2 = _rows(z)
+    dz = torch.empty_like(z)
+    call("teeny_swiglu_bwd", _p(grad), _p(z), _p(dz), M, F2 // 2, _code(z), _stream())
+    return dz
+
+
+class SwigluFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, z):
+        ctx.save_for_backward(z)
+        return swiglu(z)
+
+    @staticmethod
+    def backward(ctx, g):
+        (z,) = ctx.saved_tensors
+        return swiglu_bwd(g.contiguous(), z)
+
+
+def token_embed(ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """ids [...] (int32 or the reference's f32 encoding) -> weight rows [..., d_model]."""
+    _dev(ids, weight)
+    if ids.dtype == torch.int32:
+        idc = TEENY_I32
+    elif ids.dtype == torch.float32:
+        idc = TEENY_F32
+    else:
+        raise TypeError("ids must be int32 or float32")
+    V, Dm = weight.shape
+    out = torch.empty(ids.shape + (Dm,), dtype=weight.dtype, device=weight.device)
+    call("teeny_token_embed_fwd", _p(ids), _p(weight), _p(out), ids.numel(), Dm, V, idc,
+         _code(weight), _stream())
+    return out

@@ -1,0 +1,78 @@
+"""The C-ABI library without a GPU: it loads, exports every declared symbol,
+and rejects bad arguments with the documented codes before launching
+anything (validation runs before any HIP call)."""
+import ctypes
+
+import pytest
+
+from teenyformers_amd import _lib
+
+OK, NULLP, SHAPE, UNSUP, WS, VALUE = 0, -1, -2, -3, -4, -7
+F32, BF16 = 0, 1
+NEG_INF = float("-inf")
+P = 0x1000  # a non-null dummy pointer: never dereferenced by failing calls
+
+
+@pytest.fixture(scope="module")
+def L():
+    return _lib.lib()
+
+
+def test_exports_every_declared_symbol(L):
+    declared = _lib.header_functions()
+    assert len(declared) >= 20
+    for name in declared:
+        assert hasattr(L, name), name
+    assert L.teeny_abi_version() == 1
+
+
+def test_strerror(L):
+    assert L.teeny_strerror(0).decode() == "ok"
+    assert "workspace" in L.teeny_strerror(WS).decode()
+
+
+def fwd(L, **kw):
+    a = dict(q=P, k=P, v=P, o=P, l=P, nq=128, nk=128, scale=0.125, neg_inf=NEG_INF, b=1, hq=4,
+             hkv=4, d=64, dtype=BF16)
+    a.update(kw)
+    return L.teeny_causal_flash_attn2_fwd(a["q"], a["k"], a["v"], a["o"], a["l"], a["nq"], a["nk"],
+                                          a["scale"], a["neg_inf"], a["b"], a["hq"], a["hkv"],
+                                          a["d"], a["dtype"], None)
+
+
+def test_fa2_fwd_validation(L):
+    assert fwd(L, q=None) == NULLP
+    assert fwd(L, l=None) == NULLP
+    assert fwd(L, nq=0) == SHAPE
+    assert fwd(L, hq=6, hkv=4) == SHAPE  # Hq must be a multiple of Hkv
+    assert fwd(L, d=96) == UNSUP
+    assert fwd(L, d=32, dtype=BF16) == UNSUP  # bf16 built for 64/128
+    assert fwd(L, dtype=7) == UNSUP
+    assert fwd(L, neg_inf=-1e9) == VALUE  # the reference always passes -inf
+    assert fwd(L, scale=float("nan")) == VALUE
+
+
+def test_fa2_bwd_workspace(L):
+    need = L.teeny_flash_attn2_bwd_workspace_bytes(4096, 8, 32, 128, BF16)
+    rows = 8 * 32 * 4096
+    assert need >= rows * 4 + rows * 128 * 4
+    assert L.teeny_flash_attn2_bwd_workspace_bytes(128, 1, 4, 64, F32) >= 4 * 128 * 4
+    small = L.teeny_flash_attn2_bwd_workspace_bytes(128, 1, 4, 64, BF16)
+    rc = L.teeny_causal_flash_attn2_bwd(P, P, P, P, P, P, P, P, P, 128, 128, 0.125, 1, 4, 4, 64,
+                                        BF16, P, small - 1, None)
+    assert rc == WS
+    rc = L.teeny_causal_flash_attn2_bwd(P, P, P, P, P, P, P, P, P, 128, 128, 0.125, 1, 4, 4, 64,
+                                        BF16, None, 1 << 30, None)
+    assert rc == WS
+
+
+def test_other_ops_validation(L):
+    assert L.teeny_rope_fwd(P, P, 8, 9.21, 2, 12, BF16, None) == UNSUP  # 12 % 8
+    assert L.teeny_rope_fwd(None, P, 8, 9.21, 2, 16, F32, None) == NULLP
+    assert L.teeny_transpose_heads(P, P, 0, 4, 1, 64, BF16, None) == SHAPE
+    assert L.teeny_transpose_heads(P, P, 8, 4, 1, 64, BF16, None) == VALUE  # src == dst
+    assert L.teeny_rmsnorm_fwd(P, P, None, P, 4, 64 * 8 * 32, 1e-5, BF16, None) == UNSUP
+    assert L.teeny_fused_add_rmsnorm_fwd(P, P, P, P, None, P, 4, 16, 1e-6, F32, None) == NULLP
+    assert L.teeny_fused_add_rmsnorm_bwd(P, P, P, P, P, P, P, 4, 16, F32, None, 0, None) == WS
+    assert L.teeny_swiglu_fwd(P, P, 0, 8, F32, None) == SHAPE
+    assert L.teeny_token_embed_fwd(P, P, P, 4, 16, 10, BF16, F32, None) == UNSUP  # ids dtype

@@ -1,0 +1,213 @@
+"""GPU parity of flash-attention 2 (forward and backward) against the oracle.
+
+fp32 path: max abs <= 1e-5 against the oracle's fp32 restatement of the
+reference kernels.  bf16 path: max abs <= 2e-2 and rel-L2 <= 5e-3 for O and
+dQ/dK/dV against the fp32 oracle run on the same bf16-rounded inputs; LSE
+(fp32 output) within 2e-2.  Full benchmark shapes are checked on sampled
+heads and row slices (the oracle's q_offset keeps the causal positions).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from teenyformers_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-5
+BF16_MAX_ABS = 2e-2
+BF16_REL_L2 = 5e-3
+
+
+def randn(seed, *shape):
+    return np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+
+
+def dev(a, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda").to(dtype)
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+def rel_l2(got, want):
+    return float(np.linalg.norm((got - want).ravel()) / max(np.linalg.norm(want.ravel()), 1e-30))
+
+
+def check_bf16(name, got, want, max_abs=BF16_MAX_ABS, rel=BF16_REL_L2):
+    err = float(np.abs(got - want).max())
+    r = rel_l2(got, want)
+    assert err <= max_abs and r <= rel, f"{name}: max abs {err:.3e}, rel-L2 {r:.3e}"
+
+
+def inputs(seed, B, Hq, Hkv, Sq, Sk, D, bf16, spike=False):
+    q, k, v, do = (randn(seed, B, Hq, Sq, D), randn(seed + 1, B, Hkv, Sk, D),
+                   randn(seed + 2, B, Hkv, Sk, D), randn(seed + 3, B, Hq, Sq, D))
+    if spike:  # 1% of K rows x8 stresses the running max
+        rows = np.random.default_rng(seed + 4).choice(Sk, max(1, Sk // 100), replace=False)
+        k[:, :, rows] *= 8
+    if bf16:
+        q, k, v, do = (O.bf16_round(t) for t in (q, k, v, do))
+    return q, k, v, do
+
+
+# ---------------------------------------------------------------------------
+# fp32: the reference's precision
+# ---------------------------------------------------------------------------
+
+def test_c1_rope_transpose_fa2_f32(cuda):
+    """B1 H4 S128 D64: RoPE (theta 1e4) + [B,S,H,D]->[B,H,S,D] + causal FA2."""
+    B, S, H, D = 1, 128, 4, 64
+    qs, ks, vs = randn(100, B, S, H * D), randn(101, B, S, H * D), randn(102, B, S, H * D)
+    lnb = float(np.log(np.float32(1e4)).astype(np.float32))
+    q = ops.rope(ops.transpose_heads(dev(qs, torch.float32), H), 1e4)
+    k = ops.rope(ops.transpose_heads(dev(ks, torch.float32), H), 1e4)
+    v = ops.transpose_heads(dev(vs, torch.float32), H)
+    o, lse = ops.flash_attn2_fwd(q, k, v, 1.0 / math.sqrt(D), causal=True)
+    qe = O.rope(O.transpose_heads(qs, B, S, H, D), lnb)
+    ke = O.rope(O.transpose_heads(ks, B, S, H, D), lnb)
+    ve = O.transpose_heads(vs, B, S, H, D)
+    oe, le = O.fa2_fwd(qe, ke, ve, 1.0 / math.sqrt(D), True)
+    assert np.abs(host(o) - oe).max() <= F32_TOL
+    assert np.abs(host(lse) - le).max() <= F32_TOL
+
+
+F32_SHAPES = [  # B, Hq, Hkv, Sq, Sk, D
+    (1, 4, 4, 128, 128, 64),
+    (2, 4, 2, 77, 77, 32),
+    (1, 2, 1, 40, 90, 16),
+    (1, 2, 2, 90, 40, 128),
+    (1, 3, 3, 65, 65, 8),
+]
+
+
+@pytest.mark.parametrize("shape", F32_SHAPES)
+@pytest.mark.parametrize("causal", [True, False])
+def test_fa2_f32_fwd_bwd(cuda, shape, causal):
+    B, Hq, Hkv, Sq, Sk, D = shape
+    q, k, v, do = inputs(10, *shape, bf16=False)
+    scale = 1.0 / math.sqrt(D)
+    qd, kd, vd, dod = (dev(t, torch.float32) for t in (q, k, v, do))
+    o, lse = ops.flash_attn2_fwd(qd, kd, vd, scale, causal)
+    oe, le = O.fa2_fwd(q, k, v, scale, causal)
+    assert np.abs(host(o) - oe).max() <= F32_TOL
+    assert np.abs(host(lse) - le).max() <= F32_TOL
+    dq, dk, dv = ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod, scale, causal)
+    dqe, dke, dve = O.fa2_bwd(q, k, v, oe, do, le, scale, causal)
+    for name, got, want in (("dq", dq, dqe), ("dk", dk, dke), ("dv", dv, dve)):
+        err = np.abs(host(got) - want).max()
+        assert err <= F32_TOL * max(1.0, np.abs(want).max()), f"{name} {err}"
+
+
+# ---------------------------------------------------------------------------
+# bf16 MFMA path
+# ---------------------------------------------------------------------------
+
+BF16_SHAPES = [  # B, Hq, Hkv, Sq, Sk, D
+    (1, 4, 4, 128, 128, 64),
+    (2, 8, 2, 300, 300, 128),   # GQA 4, ragged
+    (1, 8, 1, 513, 513, 128),   # GQA 8 (MQA), ragged past a tile
+    (2, 4, 4, 256, 256, 64),
+    (1, 4, 2, 100, 300, 128),   # Sq < Sk
+    (1, 4, 2, 300, 100, 64),    # Sq > Sk
+    (1, 2, 2, 1, 1, 64),        # one row
+    (1, 2, 2, 1024, 1024, 128),
+]
+
+
+@pytest.mark.parametrize("shape", BF16_SHAPES)
+@pytest.mark.parametrize("causal", [True, False])
+def test_fa2_bf16_fwd(cuda, shape, causal):
+    B, Hq, Hkv, Sq, Sk, D = shape
+    q, k, v, _ = inputs(20, *shape, bf16=True, spike=True)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = ops.flash_attn2_fwd(dev(q, torch.bfloat16), dev(k, torch.bfloat16),
+                                 dev(v, torch.bfloat16), scale, causal)
+    oe, le = O.fa2_fwd(q, k, v, scale, causal)
+    check_bf16("O", host(o), oe)
+    assert np.abs(host(lse) - le).max() <= 2e-2
+
+
+@pytest.mark.parametrize("shape", BF16_SHAPES)
+@pytest.mark.parametrize("causal", [True, False])
+def test_fa2_bf16_bwd(cuda, shape, causal):
+    B, Hq, Hkv, Sq, Sk, D = shape
+    q, k, v, do = inputs(30, *shape, bf16=True)
+    scale = 1.0 / math.sqrt(D)
+    qd, kd, vd, dod = (dev(t, torch.bfloat16) for t in (q, k, v, do))
+    o, lse = ops.flash_attn2_fwd(qd, kd, vd, scale, causal)
+    dq, dk, dv = ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod, scale, causal)
+    oe, le = O.fa2_fwd(q, k, v, scale, causal)
+    dqe, dke, dve = O.fa2_bwd(q, k, v, oe, do, le, scale, causal)
+    check_bf16("dQ", host(dq), dqe)
+    check_bf16("dK", host(dk), dke)
+    check_bf16("dV", host(dv), dve)
+
+
+def test_fa2_bf16_bwd_deterministic(cuda):
+    q, k, v, do = inputs(40, 1, 8, 2, 700, 700, 128, bf16=True)
+    qd, kd, vd, dod = (dev(t, torch.bfloat16) for t in (q, k, v, do))
+    o, lse = ops.flash_attn2_fwd(qd, kd, vd)
+    a = ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod)
+    b = ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod)
+    # dK/dV are register accumulations in a fixed order
+    assert torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])
+
+
+# ---------------------------------------------------------------------------
+# Full benchmark shapes, sampled
+# ---------------------------------------------------------------------------
+
+def _sampled_check(B, Hq, Hkv, S, D, seed, spike, rows):
+    """Run fwd+bwd at full size on the GPU; check row slices of sampled heads.
+
+    rows: list of (start, stop) query-row slices.  For a slice starting at a,
+    dQ of those rows and dK/dV of keys >= a depend only on rows >= a (causal),
+    so the oracle evaluates them with q_offset = a.
+    """
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    shape_q, shape_kv = (B, Hq, S, D), (B, Hkv, S, D)
+    q = torch.randn(shape_q, generator=gen, device="cuda").to(torch.bfloat16)
+    k = torch.randn(shape_kv, generator=gen, device="cuda")
+    if spike:
+        idx = torch.randperm(S, generator=gen, device="cuda")[: max(1, S // 100)]
+        k[:, :, idx] *= 8
+    k = k.to(torch.bfloat16)
+    v = torch.randn(shape_kv, generator=gen, device="cuda").to(torch.bfloat16)
+    do = torch.randn(shape_q, generator=gen, device="cuda").to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = ops.flash_attn2_fwd(q, k, v, scale, True)
+    dq, dk, dv = ops.flash_attn2_bwd(q, k, v, o, lse, do, scale, True)
+    torch.cuda.synchronize()
+    group = Hq // Hkv
+    for b, hk in ((0, 0), (B - 1, Hkv - 1)):
+        hs = slice(hk * group, (hk + 1) * group)
+        kk, vv = host(k[b:b + 1, hk:hk + 1]), host(v[b:b + 1, hk:hk + 1])
+        for a, z in rows:
+            qq = host(q[b:b + 1, hs, a:z])
+            dd = host(do[b:b + 1, hs, a:z])
+            oe, le = O.fa2_fwd(qq, kk, vv, scale, True, q_offset=a)
+            check_bf16(f"O[{b},{hk},{a}:{z}]", host(o[b:b + 1, hs, a:z]), oe)
+            assert np.abs(host(lse[b:b + 1, hs, a:z]) - le).max() <= 2e-2
+            if z == S:  # a tail slice: dK/dV of keys >= a are complete
+                dqe, dke, dve = O.fa2_bwd(qq, kk, vv, oe, dd, le, scale, True, q_offset=a)
+                check_bf16("dQ", host(dq[b:b + 1, hs, a:z]), dqe)
+                check_bf16("dK", host(dk[b:b + 1, hk:hk + 1, a:]), dke[:, :, a:])
+                check_bf16("dV", host(dv[b:b + 1, hk:hk + 1, a:]), dve[:, :, a:])
+    assert torch.isfinite(dq.float()).all() and torch.isfinite(dk.float()).all()
+
+
+def test_fa2_bf16_c3_full_size_sampled(cuda):
+    """B8 H32 S4096 D128 causal, the headline shape."""
+    _sampled_check(8, 32, 32, 4096, 128, seed=7, spike=False,
+                   rows=[(0, 256), (2000, 2100), (3840, 4096)])
+
+
+@pytest.mark.parametrize("S", [16384, 8191])
+def test_fa2_bf16_c5_long_gqa_sampled(cuda, S):
+    """B1 Hq64 Hkv8 D128 causal, 1% of K rows x8; S = 16384 and ragged 8191."""
+    _sampled_check(1, 64, 8, S, 128, seed=8, spike=True, rows=[(0, 128), (S - 192, S)])
