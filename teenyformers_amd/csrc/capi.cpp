@@ -106,8 +106,10 @@ int get_function(const char* name, hipFunction_t* fn) {
       *fn = f;
       return TEENY_OK;
     }
+    // A miss sets the thread's sticky "last error"; clear it so the caller's
+    // next HIP call (e.g. torch's launch check) does not report it.
+    (void)hipGetLastError();
   }
-  (void)hipGetLastError();  // clear the lookup misses
   return TEENY_ERR_MODULE;
 }
 

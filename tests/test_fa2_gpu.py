@@ -1,9 +1,11 @@
 """GPU parity of flash-attention 2 (forward and backward) against the oracle.
 
 fp32 path: max abs <= 1e-5 against the oracle's fp32 restatement of the
-reference kernels.  bf16 path: max abs <= 2e-2 and rel-L2 <= 5e-3 for O and
-dQ/dK/dV against the fp32 oracle run on the same bf16-rounded inputs; LSE
-(fp32 output) within 2e-2.  Full benchmark shapes are checked on sampled
+reference kernels.  bf16 path: rel-L2 <= 5e-3 and max abs <= 2e-2 (scaled by
+the tensor's magnitude above 4, see check_bf16) for O and dQ/dK/dV against
+the fp32 oracle run on the same bf16-rounded inputs; LSE (fp32) within 2e-2.
+Each op is compared on its own inputs: the backward's oracle receives the
+same O and LSE the GPU backward received.  Full benchmark shapes are checked on sampled
 heads and row slices (the oracle's q_offset keeps the causal positions).
 """
 import math
@@ -38,10 +40,19 @@ def rel_l2(got, want):
     return float(np.linalg.norm((got - want).ravel()) / max(np.linalg.norm(want.ravel()), 1e-30))
 
 
-def check_bf16(name, got, want, max_abs=BF16_MAX_ABS, rel=BF16_REL_L2):
+def check_bf16(name, got, want):
+    """bf16 bar: rel-L2 <= 5e-3 and max abs <= 2e-2 * max(1, max|want| / 4).
+
+    The flat 2e-2 is 2.5 bf16 half-ulps at magnitude 4.  A bf16 output of
+    magnitude M cannot sit closer than M * 2^-9 to its fp32 value, so for
+    tensors larger than 4 (GQA-summed dK/dV, dQ of the 8x-spiked keys, whose
+    values reach 30) the max-abs bar scales with M; unit-scale tensors, such
+    as every output at the B8 H32 S4096 D128 shape, get the flat 2e-2.
+    """
     err = float(np.abs(got - want).max())
     r = rel_l2(got, want)
-    assert err <= max_abs and r <= rel, f"{name}: max abs {err:.3e}, rel-L2 {r:.3e}"
+    bar = BF16_MAX_ABS * max(1.0, float(np.abs(want).max()) / 4.0)
+    assert err <= bar and r <= BF16_REL_L2, f"{name}: max abs {err:.3e} (bar {bar:.3e}), rel-L2 {r:.3e}"
 
 
 def inputs(seed, B, Hq, Hkv, Sq, Sk, D, bf16, spike=False):
@@ -141,8 +152,8 @@ def test_fa2_bf16_bwd(cuda, shape, causal):
     qd, kd, vd, dod = (dev(t, torch.bfloat16) for t in (q, k, v, do))
     o, lse = ops.flash_attn2_fwd(qd, kd, vd, scale, causal)
     dq, dk, dv = ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod, scale, causal)
-    oe, le = O.fa2_fwd(q, k, v, scale, causal)
-    dqe, dke, dve = O.fa2_bwd(q, k, v, oe, do, le, scale, causal)
+    # the backward op's inputs include O and LSE: the oracle gets the same ones
+    dqe, dke, dve = O.fa2_bwd(q, k, v, host(o), do, host(lse), scale, causal)
     check_bf16("dQ", host(dq), dqe)
     check_bf16("dK", host(dk), dke)
     check_bf16("dV", host(dv), dve)
@@ -194,7 +205,9 @@ def _sampled_check(B, Hq, Hkv, S, D, seed, spike, rows):
             check_bf16(f"O[{b},{hk},{a}:{z}]", host(o[b:b + 1, hs, a:z]), oe)
             assert np.abs(host(lse[b:b + 1, hs, a:z]) - le).max() <= 2e-2
             if z == S:  # a tail slice: dK/dV of keys >= a are complete
-                dqe, dke, dve = O.fa2_bwd(qq, kk, vv, oe, dd, le, scale, True, q_offset=a)
+                # the backward's inputs include O and LSE: give the oracle the same ones
+                og, lg = host(o[b:b + 1, hs, a:z]), host(lse[b:b + 1, hs, a:z])
+                dqe, dke, dve = O.fa2_bwd(qq, kk, vv, og, dd, lg, scale, True, q_offset=a)
                 check_bf16("dQ", host(dq[b:b + 1, hs, a:z]), dqe)
                 check_bf16("dK", host(dk[b:b + 1, hk:hk + 1, a:]), dke[:, :, a:])
                 check_bf16("dV", host(dv[b:b + 1, hk:hk + 1, a:]), dve[:, :, a:])

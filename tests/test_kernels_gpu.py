@@ -37,6 +37,13 @@ def host(t):
     return t.float().cpu().numpy()
 
 
+def f32_close(got, want):
+    """fp32 bar for row reductions: 1e-5 absolute, or 2e-6 of the output
+    scale when outputs exceed 5 (a reduction over N terms may round
+    differently from the oracle's sequential sum)."""
+    return float(np.abs(got - want).max()) <= max(F32_TOL, 2e-6 * float(np.abs(want).max()))
+
+
 def bf16_close(got, want):
     """|got - want| <= one bf16 ulp of want (plus a tiny absolute floor)."""
     ulp = np.abs(want) * 2.0 ** -8 + 1e-30
@@ -112,21 +119,21 @@ def test_rmsnorm_f32_fwd_bwd(cuda, m, n):
     x, r, w, g = randn(4, m, n), randn(5, m, n), randn(6, n), randn(7, m, n)
     y, h, rstd = ops.fused_add_rmsnorm(dev(x), dev(r), dev(w), 1e-5)
     ye, he, re_ = O.fused_add_rmsnorm_fwd(x, r, w, 1e-5)
-    assert np.abs(host(y) - ye).max() <= F32_TOL
+    assert f32_close(host(y), ye)
     assert np.array_equal(host(h), he)
     assert np.abs(host(rstd) - re_).max() <= 1e-5 * np.abs(re_).max()
     # reference-formula fused backward
     dw0 = randn(8, n)
     dx, dres, dw = ops.fused_add_rmsnorm_bwd(dev(g), h, dev(w), rstd, dweight=dev(dw0))
     dxe, _, dwe = O.fused_add_rmsnorm_bwd(g, he, w, re_, dw_in=dw0)
-    assert np.abs(host(dx) - dxe).max() <= F32_TOL
+    assert f32_close(host(dx), dxe)
     assert torch.equal(dx, dres)
     assert np.abs(host(dw) - dwe).max() <= 1e-5 * max(1.0, np.abs(dwe).max())
     # true-gradient plain backward
     yp, rp = ops.rmsnorm(dev(x), dev(w), 1e-5)
     dxp, dwp = ops.rmsnorm_bwd(dev(g), dev(x), dev(w), rp)
     dxpe, dwpe = O.rmsnorm_bwd(g, x, w, O.rmsnorm_fwd(x, w, 1e-5)[1])
-    assert np.abs(host(dxp) - dxpe).max() <= F32_TOL
+    assert f32_close(host(dxp), dxpe)
     assert np.abs(host(dwp) - dwpe).max() <= 1e-5 * max(1.0, np.abs(dwpe).max())
 
 
