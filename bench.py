@@ -1,0 +1,196 @@
+"""Benchmark of the attention hot path on one MI355X.
+
+A step is one causal flash-attention-2 forward + backward (bf16 in, fp32
+accumulate) over B=8, H=32 (MHA), S=4096, D=128, the headline shape; inputs
+are resident in HBM before timing.  Prints one JSON line:
+  value       whole-step throughput in TFLOP/s (algorithmic: causal forward
+              4*B*H*S^2*D/2, backward 2.5x that)
+  roofline    the dominant kernel (most summed time) measured with HIP events
+              recorded on its launch stream during the timed steps
+  cpu_baseline the oracle's restatement of the reference kernels (fp32,
+              every key of every row, as the reference loops) timed on a
+              sample of heads on this host's cores
+  detail      per-op numbers (forward, backward, each kernel)
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "FA2 fwd+bwd TFLOP/s & %MFMA peak; Llama-8B-shape prefill tokens/s, 1 GPU"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+B, H, S, D = 8, 32, 4096, 128
+
+
+def fwd_flops(b, hq, sq, sk, d, causal=True):
+    return 4.0 * b * hq * sq * sk * d * (0.5 if causal else 1.0)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=4,
+                    help="heads of the workload the CPU baseline times")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(attention shards over (batch, kv-head) with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from teenyformers_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _lib.lib()
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    shape = (B, H, S, D)
+    q, k, v, do = (torch.randn(shape, generator=gen, device=dev).to(torch.bfloat16)
+                   for _ in range(4))
+    scale = 1.0 / math.sqrt(D)
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = torch.empty(ops.flash_attn2_bwd_workspace_bytes(q), dtype=torch.uint8, device=dev)
+
+    def step():
+        ops.flash_attn2_fwd(q, k, v, scale, True, out=o, lse=lse)
+        ops.flash_attn2_bwd(q, k, v, o, lse, do, scale, True, workspace=ws, dq=dq, dk=dk, dv=dv)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    _lib.profile_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    _lib.profile_enable(False)
+    stats = _lib.profile_stats()
+
+    f_fwd = fwd_flops(B, H, S, S, D)
+    f_bwd = 2.5 * f_fwd
+    ms_step = elapsed * 1e3 / args.steps
+    value = (f_fwd + f_bwd) / (ms_step * 1e-3) / 1e12
+
+    kernels = {}
+    for name, (n, tot) in stats.items():
+        kernels[name] = {"launches": n, "avg_ms": tot / max(n, 1), "total_ms": tot}
+    # Algorithmic MFMA work of each kernel, in units of the forward's
+    # 2 products (QK^T, PV): the dK/dV kernel does S, dP, dV, dK (2.0x fwd),
+    # the dQ kernel S, dP, dQ (1.5x fwd); the backward as a whole is credited
+    # the 5 products (2.5x fwd) of the FA2 convention.
+    work = {"teeny_fa2_fwd_bf16": f_fwd, "teeny_fa2_bwd_dkdv_bf16": 2.0 * f_fwd,
+            "teeny_fa2_bwd_dq_bf16": 1.5 * f_fwd}
+    fwd_ms = sum(kernels[n]["avg_ms"] for n in kernels if n.startswith("teeny_fa2_fwd_bf16"))
+    bwd_all_ms = sum(kernels[n]["avg_ms"] for n in kernels if n.startswith("teeny_fa2_bwd"))
+    dominant = max((n for n in kernels if any(n.startswith(p) for p in work)),
+                   key=lambda n: kernels[n]["total_ms"])
+    dom_flops = next(w for p, w in work.items() if dominant.startswith(p))
+    dom_ms = kernels[dominant]["avg_ms"]
+    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+    for name in kernels:
+        kernels[name]["avg_ms"] = round(kernels[name]["avg_ms"], 4)
+        kernels[name]["total_ms"] = round(kernels[name]["total_ms"], 3)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "causal flash-attention-2 forward+backward, MHA",
+                   "batch": B, "heads": H, "seq_len": S, "head_dim": D, "causal": True,
+                   "flop_per_step": f_fwd + f_bwd},
+        "roofline": {"bound": "mfma", "kernel": dominant,
+                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": None,
+        "detail": {
+            "pct_mfma_peak_step": round(value / PEAK_BF16_TFLOPS, 4),
+            "fwd_tflops": round(f_fwd / (fwd_ms * 1e-3) / 1e12, 2) if fwd_ms else None,
+            "fwd_pct_peak": round(f_fwd / (fwd_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
+            if fwd_ms else None,
+            "bwd_tflops": round(f_bwd / (bwd_all_ms * 1e-3) / 1e12, 2) if bwd_all_ms else None,
+            "bwd_pct_peak": round(f_bwd / (bwd_all_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
+            if bwd_all_ms else None,
+            "kernels": kernels,
+        },
+    }
+
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(q, k, v, do, scale, args.cpu_heads)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def cpu_baseline(q, k, v, do, scale, n_heads):
+    """Time the oracle (fp32 restatement of the reference kernels, every key of
+    every query row like the reference's loop) on n_heads (b, h) slices of the
+    same inputs, and report TFLOP/s with the same algorithmic FLOP count."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    picks = [(i * B // n_heads, (i * 7) % H) for i in range(n_heads)]
+    sel = lambda t: np.stack([t[b, h].float().cpu().numpy() for b, h in picks])[None]  # noqa
+    qs, ks, vs, dos = sel(q), sel(k), sel(v), sel(do)
+    threads = O.num_threads()
+    t0 = time.perf_counter()
+    o, lse = O.fa2_fwd(qs, ks, vs, scale, True, all_keys=True)
+    t1 = time.perf_counter()
+    O.fa2_bwd(qs, ks, vs, o, dos, lse, scale, True, all_keys=True)
+    t2 = time.perf_counter()
+    f_fwd = fwd_flops(1, n_heads, S, S, D)
+    f_tot = 3.5 * f_fwd
+    return {
+        "value": round(f_tot / (t2 - t0) / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"fwd+bwd of {n_heads} of the {B * H} (b, h) heads at S={S}, D={D}, fp32; "
+                  f"fwd {t1 - t0:.2f} s, bwd {t2 - t1:.2f} s",
+        "cpu": _cpu_model(),
+    }
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -52,6 +52,16 @@ int teeny_last_hip_error(void);
 /* Load the code objects on the current device (optional: done lazily). */
 int teeny_init(void);
 
+/* Launch profiler (no counterpart in the reference, which has no tracing).
+ * teeny_profile_enable(1) clears the records and brackets every following
+ * launch with two hipEvents recorded on the launch's own stream;
+ * teeny_profile_enable(0) stops recording.  kernel_stats synchronises on the
+ * recorded events of one kernel symbol and returns its launch count and
+ * summed duration; kernel_names lists the recorded symbols, one per line. */
+int teeny_profile_enable(int on);
+int teeny_profile_kernel_stats(const char* kernel_name, int* launches, double* total_ms);
+int teeny_profile_kernel_names(char* buf, size_t buf_bytes);
+
 /* --------------------------------------------------------------------------
  * Flash attention 2
  *
@@ -100,8 +110,8 @@ int teeny_flash_attn2_bwd(const void* q, const void* k, const void* v, const voi
                           int n_heads_kv, int head_dim, int dtype, void* workspace,
                           size_t workspace_bytes, hipStream_t stream);
 
-/* Workspace the backward needs: Delta [B*Hq, n_ctx_q] fp32, plus for bf16 a
- * dQ accumulator [B*Hq, n_ctx_q, D] fp32.  No counterpart in the reference
+/* Workspace the backward needs: Delta = rowsum(O * dO) [B*Hq, n_ctx_q] fp32.
+ * No counterpart in the reference
  * (its executor sizes caches from RuntimeOp::param_shapes, flash_attn2.rs:449-457). */
 size_t teeny_flash_attn2_bwd_workspace_bytes(int n_ctx_q, int batch, int n_heads_q, int head_dim,
                                              int dtype);

@@ -38,6 +38,10 @@ _SIGNATURES = {
     "teeny_strerror": ([_i], ctypes.c_char_p),
     "teeny_last_hip_error": ([], _i),
     "teeny_init": ([], _i),
+    "teeny_profile_enable": ([_i], _i),
+    "teeny_profile_kernel_stats": ([ctypes.c_char_p, ctypes.POINTER(_i),
+                                    ctypes.POINTER(ctypes.c_double)], _i),
+    "teeny_profile_kernel_names": ([ctypes.c_char_p, _sz], _i),
     "teeny_causal_flash_attn2_fwd": ([_p] * 5 + [_i, _i, _f, _f, _i, _i, _i, _i, _i, _p], _i),
     "teeny_flash_attn2_fwd": ([_p] * 5 + [_i, _i, _f, _f, _i, _i, _i, _i, _i, _p], _i),
     "teeny_causal_flash_attn2_bwd": ([_p] * 9 + [_i, _i, _f, _i, _i, _i, _i, _i, _p, _sz, _p], _i),
@@ -90,6 +94,23 @@ def check(rc: int, what: str) -> None:
 def call(name: str, *args) -> None:
     """Call a status-returning entry point and raise on a nonzero status."""
     check(getattr(lib(), name)(*args), name)
+
+
+def profile_enable(on: bool) -> None:
+    call("teeny_profile_enable", int(bool(on)))
+
+
+def profile_stats() -> dict[str, tuple[int, float]]:
+    """{kernel symbol: (launches, total ms)} for the launches recorded since
+    profile_enable(True).  Synchronises on the recorded events."""
+    buf = ctypes.create_string_buffer(1 << 16)
+    call("teeny_profile_kernel_names", buf, len(buf))
+    out = {}
+    for name in buf.value.decode().split():
+        n, ms = _i(), ctypes.c_double()
+        call("teeny_profile_kernel_stats", name.encode(), ctypes.byref(n), ctypes.byref(ms))
+        out[name] = (n.value, ms.value)
+    return out
 
 
 def header_functions() -> list[str]:

@@ -10,7 +10,8 @@ Steps:
      the HIP runtime; the host library has no device code of its own).
 
 Every HIP file is compiled with packed-fp32 instruction selection disabled
-(-packed-fp32-ops): the kernels' fp32 math is issued as scalar VALU ops.
+(-packed-fp32-ops): the kernels' fp32 math is issued as scalar VALU ops; and
+with MFMA operands in VGPR form (see HIPCC_FLAGS).
 """
 from __future__ import annotations
 
@@ -38,6 +39,10 @@ HIPCC_FLAGS = [
     "-O3", "-std=c++17", f"--offload-arch={ARCH}", "--genco",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-munsafe-fp-atomics", "-ffp-contract=fast",
+    # keep MFMA accumulators in the VGPR file: with AGPR accumulators the
+    # loop-carried dK/dV sums were copied between register files every
+    # iteration
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wno-unused-result",
 ]
 

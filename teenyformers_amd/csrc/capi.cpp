@@ -18,6 +18,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 // ---------------------------------------------------------------------------
 // Embedded code objects (symbols defined by the generated co_blob.S)
@@ -113,14 +114,61 @@ int get_function(const char* name, hipFunction_t* fn) {
   return TEENY_ERR_MODULE;
 }
 
+// ---------------------------------------------------------------------------
+// Opt-in launch profiler: while enabled, every launch is bracketed by two
+// hipEvents recorded on its own stream; durations are read (synchronising on
+// the events) only when stats are requested.
+// ---------------------------------------------------------------------------
+struct ProfRecord {
+  std::string name;
+  hipEvent_t start, stop;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<ProfRecord> g_prof;
+std::vector<hipEvent_t> g_event_pool;
+
+hipEvent_t pool_event() {
+  if (!g_event_pool.empty()) {
+    hipEvent_t e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+void prof_clear_locked() {
+  for (auto& r : g_prof) {
+    g_event_pool.push_back(r.start);
+    g_event_pool.push_back(r.stop);
+  }
+  g_prof.clear();
+}
+
 int launch(const char* name, dim3 grid, dim3 block, unsigned shmem, hipStream_t stream,
            void** args) {
   if (grid.x == 0 || grid.y == 0 || grid.z == 0) return TEENY_OK;  // nothing to do
   hipFunction_t f = nullptr;
   int rc = get_function(name, &f);
   if (rc) return rc;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    if (g_prof_on) {
+      ev0 = pool_event();
+      ev1 = pool_event();
+    }
+  }
+  if (ev0 && ev1) (void)hipEventRecord(ev0, stream);
   hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
                                        shmem, stream, args, nullptr);
+  if (ev0 && ev1) {
+    (void)hipEventRecord(ev1, stream);
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    g_prof.push_back({name, ev0, ev1});
+  }
   if (e != hipSuccess) return hip_fail(e);
   return TEENY_OK;
 }
@@ -178,10 +226,9 @@ int fa2_fwd(bool causal, const void* q, const void* k, const void* v, void* o, f
 }
 
 size_t fa2_bwd_ws(int n_ctx_q, int batch, int hq, int head_dim, int dtype) {
-  size_t rows = (size_t)batch * hq * n_ctx_q;
-  size_t ws = align256(rows * sizeof(float));
-  if (dtype == TEENY_BF16) ws += align256(rows * head_dim * sizeof(float));
-  return ws;
+  (void)head_dim;
+  (void)dtype;
+  return align256((size_t)batch * hq * n_ctx_q * sizeof(float));  // Delta
 }
 
 int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void* o,
@@ -199,26 +246,31 @@ int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void
   const char* cz = causal ? "c" : "n";
   char name[64];
   if (dtype == TEENY_BF16) {
-    float* dq_acc = (float*)((char*)workspace + align256(rows * sizeof(float)));
     const int rows_per_block = 256 / (head_dim / 8);
     snprintf(name, sizeof name, "teeny_fa2_bwd_pre_bf16_d%d", head_dim);
-    void* a0[] = {&o, &dout, &delta, &dq_acc, (void*)&rows};
+    void* a0[] = {&o, &dout, &delta, (void*)&rows};
     rc = launch(name, dim3((unsigned)((rows + rows_per_block - 1) / rows_per_block)), dim3(256),
                 0, stream, a0);
     if (rc) return rc;
+    // dK, dV: one workgroup per 128 keys of a (b, kv head)
     int nnb = (n_ctx_k + 127) / 128;
     long total = (long)nnb * batch * hkv;
     if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
     int tot = (int)total;
-    snprintf(name, sizeof name, "teeny_fa2_bwd_bf16_d%d_%s", head_dim, cz);
-    void* a1[] = {&q,       &k,       &v,     &dout, &l,     &delta, &dq_acc, &dk,  &dv,
-                  &n_ctx_q, &n_ctx_k, &scale, &hq,   &hkv,   &nnb,   &tot};
+    snprintf(name, sizeof name, "teeny_fa2_bwd_dkdv_bf16_d%d_%s", head_dim, cz);
+    void* a1[] = {&q,       &k,       &v,     &dout, &l,   &delta, &dk,  &dv,
+                  &n_ctx_q, &n_ctx_k, &scale, &hq,   &hkv, &nnb,   &tot};
     rc = launch(name, dim3(tot), dim3(256), 0, stream, a1);
     if (rc) return rc;
-    long n8 = rows * head_dim / 8;
-    void* a2[] = {&dq_acc, &dq, &scale, &n8};
-    return launch("teeny_fa2_bwd_dq_convert_bf16", dim3((unsigned)((n8 + 255) / 256)), dim3(256),
-                  0, stream, a2);
+    // dQ: one workgroup per 128 query rows of a (b, q head)
+    int nmb = (n_ctx_q + 127) / 128;
+    total = (long)nmb * batch * hq;
+    if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
+    tot = (int)total;
+    snprintf(name, sizeof name, "teeny_fa2_bwd_dq_bf16_d%d_%s", head_dim, cz);
+    void* a2[] = {&q,       &k,       &v,     &dout, &l,   &delta, &dq,
+                  &n_ctx_q, &n_ctx_k, &scale, &hq,   &hkv, &nmb,   &tot};
+    return launch(name, dim3(tot), dim3(256), 0, stream, a2);
   }
   snprintf(name, sizeof name, "teeny_fa2_bwd_pre_f32_d%d", head_dim);
   void* a0[] = {&o, &dout, &delta, (void*)&rows};
@@ -290,6 +342,46 @@ int teeny_init(void) {
   std::lock_guard<std::mutex> lk(g_mu);
   DeviceState* st = nullptr;
   return load_device_locked(dev, &st);
+}
+
+int teeny_profile_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof_on = on != 0;
+  if (g_prof_on) prof_clear_locked();
+  return TEENY_OK;
+}
+
+int teeny_profile_kernel_stats(const char* name, int* launches, double* total_ms) {
+  if (!name || !launches || !total_ms) return TEENY_ERR_NULL_POINTER;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  int n = 0;
+  double tot = 0.0;
+  for (auto& r : g_prof) {
+    if (r.name != name) continue;
+    hipError_t e = hipEventSynchronize(r.stop);
+    if (e != hipSuccess) return hip_fail(e);
+    float ms = 0.0f;
+    e = hipEventElapsedTime(&ms, r.start, r.stop);
+    if (e != hipSuccess) return hip_fail(e);
+    ++n;
+    tot += ms;
+  }
+  *launches = n;
+  *total_ms = tot;
+  return TEENY_OK;
+}
+
+int teeny_profile_kernel_names(char* buf, size_t buf_bytes) {
+  if (!buf || buf_bytes == 0) return TEENY_ERR_NULL_POINTER;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  std::string out;
+  for (auto& r : g_prof) {
+    std::string key = r.name + "\n";
+    if (out.find(key) == std::string::npos) out += key;
+  }
+  if (out.size() + 1 > buf_bytes) return TEENY_ERR_INVALID_SHAPE;
+  memcpy(buf, out.c_str(), out.size() + 1);
+  return TEENY_OK;
 }
 
 int teeny_causal_flash_attn2_fwd(const void* q, const void* k, const void* v, void* o, float* l,

@@ -6,18 +6,24 @@
 //   dS = P o (dP - Delta) with Delta = rowsum(O o dO), dQ = scale dS K,
 //   dK = scale dS^T Q.
 // The reference runs one CTA per query row and adds dK/dV with fp32 atomics
-// (nondeterministic).  Here the work is key-parallel:
-//   * one workgroup (4 wavefronts) owns 128 keys of one (b, kv head); each
-//     wave owns 32 keys whose K and V rows stay in registers as B operands of
-//     v_mfma_f32_32x32x16_bf16;
-//   * it walks the query blocks (32 rows) of every q head of its GQA group;
-//     Q and dO tiles are staged in LDS row-major and transposed;
-//   * dK^T and dV^T accumulate in registers across the whole walk: no
-//     atomics on dK/dV, deterministic, GQA reduction for free;
-//   * dS (bf16) goes through LDS and the block's dQ contribution
-//     (32 rows x D) is added to an fp32 workspace with one coalesced
-//     hardware float atomic per element; a last kernel scales and rounds it.
-//   * causal: query blocks entirely above the block's first key are skipped.
+// (nondeterministic).  Here the backward is three kernels, all deterministic
+// and free of atomics:
+//   1. bwd_pre: Delta = rowsum(O o dO) in fp32;
+//   2. dK/dV, key-parallel: one workgroup (4 wavefronts) owns 128 keys of one
+//      (b, kv head); each wave's 32 K rows stay in registers and its V rows in
+//      LDS as B operands of v_mfma_f32_32x32x16_bf16, and it walks the 32-row query
+//      blocks of every q head of its GQA group (Q, dO staged in LDS row-major
+//      and transposed), accumulating dK^T and dV^T in registers: the GQA
+//      reduction comes for free;
+//   3. dQ, query-parallel, shaped like the forward: each wave's Q and dO
+//      rows are B operands in registers, 32-key tiles of K, V (row-major) and
+//      K^T stream through double-buffered LDS, S^T and dP^T put one query row
+//      in each lane, and dQ^T += K^T dS^T accumulates in registers.
+// Recomputing S and dP in the dQ kernel costs 7 matrix products per tile
+// pair instead of 5; in exchange neither kernel needs dS round trips through
+// LDS, fp32 atomics or a dQ accumulator in HBM.
+// Causal: blocks entirely above the diagonal are skipped, diagonal blocks
+// are masked.
 #include "common.h"
 
 namespace {
@@ -46,22 +52,10 @@ DEVI void transpose4x8(const u32x4 (&in)[4], u32x2 (&out)[8]) {
   }
 }
 
-template <int D>
-struct __attribute__((aligned(16))) BwdSmem {
-  bf16 qs[BM][D + KPAD];     // Q tile, row-major  (A operand of S)
-  bf16 dos[BM][D + KPAD];    // dO tile, row-major (A operand of dP)
-  bf16 qts[D][BM + TPAD];    // Q tile transposed  (A operand of dK^T)
-  bf16 dots[D][BM + TPAD];   // dO tile transposed (A operand of dV^T)
-  bf16 dss[BM][BN + KPAD];   // dS tile, row-major (A operand of dQ)
-  bf16 kts[D][BN + KPAD];    // K block transposed (B operand of dQ)
-  float lse2[BM];            // LSE * log2(e); +inf for rows past nq
-  float delta[BM];
-};
-
-// Delta = rowsum(O o dO) in fp32 and zero the fp32 dQ accumulator.
+// Delta = rowsum(O o dO) in fp32.
 template <int D>
 __device__ void bwd_pre(const bf16* __restrict__ o, const bf16* __restrict__ dout,
-                        float* __restrict__ delta, float* __restrict__ dq_acc, long rows) {
+                        float* __restrict__ delta, long rows) {
   constexpr int TPR = D / 8;  // threads per row, 8 elements each
   const long row = (long)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
   const int c = threadIdx.x % TPR;
@@ -72,28 +66,39 @@ __device__ void bwd_pre(const bf16* __restrict__ o, const bf16* __restrict__ dou
     Vec16<bf16>::load(dout + row * D + 8 * c, bb);
 #pragma unroll
     for (int j = 0; j < 8; ++j) s += a[j] * bb[j];
-    f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-    *reinterpret_cast<f32x4*>(dq_acc + row * D + 8 * c) = z;
-    *reinterpret_cast<f32x4*>(dq_acc + row * D + 8 * c + 4) = z;
   }
 #pragma unroll
   for (int off = TPR / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
   if (row < rows && c == 0) delta[row] = s;
 }
 
+// ===========================================================================
+// dK / dV (key-parallel)
+// ===========================================================================
+// One buffer of Q / dO tiles (the next tile waits in registers) so that two
+// workgroups fit in a CU's LDS.
+template <int D>
+struct __attribute__((aligned(16))) DkdvSmem {
+  bf16 qs[1][BM][D + KPAD];    // Q tile, row-major  (A operand of S)
+  bf16 dos[1][BM][D + KPAD];   // dO tile, row-major (A operand of dP)
+  bf16 qts[1][D][BM + TPAD];   // Q tile transposed  (A operand of dK^T)
+  bf16 dots[1][D][BM + TPAD];  // dO tile transposed (A operand of dV^T)
+  float lse2[1][BM];           // LSE * log2(e); +inf for rows past nq
+  float delta[1][BM];
+  bf16 vs[BN][D + KPAD];       // the block's V rows (B operand of dP)
+};
+
 template <int D, bool CAUSAL>
-__device__ void fa2_bwd_bf16(const bf16* __restrict__ q, const bf16* __restrict__ k,
+__device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict__ k,
                              const bf16* __restrict__ v, const bf16* __restrict__ dout,
                              const float* __restrict__ lse, const float* __restrict__ delta,
-                             float* __restrict__ dq_acc, bf16* __restrict__ dk,
-                             bf16* __restrict__ dv, int nq, int nk, float scale, int hq, int hkv,
-                             int num_n_blocks, int total_blocks) {
+                             bf16* __restrict__ dk, bf16* __restrict__ dv, int nq, int nk,
+                             float scale, int hq, int hkv, int num_n_blocks, int total_blocks) {
   constexpr int DC = D / 16;  // d-chunks of 16 (QK^T, dO V^T)
-  constexpr int DT = D / 32;  // d-tiles of 32 (dK^T, dV^T, dQ)
+  constexpr int DT = D / 32;  // d-tiles of 32 (dK^T, dV^T)
   constexpr int CPR = D / 8;  // 16-byte chunks per row
   constexpr int TILE_PAIRS = (BM / 4) * CPR;  // (4-row, 8-col) blocks per Q (or dO) tile
-  constexpr int KT_PAIRS = (BN / 4) * CPR;    // same for the K block
-  __shared__ BwdSmem<D> sm;
+  __shared__ DkdvSmem<D> sm;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -111,32 +116,21 @@ __device__ void fa2_bwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   const bf16* kb = k + (long)kvh * nk * D;
   const bf16* vb = v + (long)kvh * nk * D;
 
-  // ---- K, V rows of this lane's key -> registers (B operands) --------------
-  bf16x8 kreg[DC], vreg[DC];
+  // ---- K rows of this lane's key -> registers (B operand of S) ------------
+  bf16x8 kreg[DC];
   {
     const bool ok = mykey < nk;
     const bf16* kp = kb + (long)(ok ? mykey : 0) * D + 8 * g;
-    const bf16* vp = vb + (long)(ok ? mykey : 0) * D + 8 * g;
 #pragma unroll
-    for (int c = 0; c < DC; ++c) {
+    for (int c = 0; c < DC; ++c)
       kreg[c] = as_bf16x8(ok ? *reinterpret_cast<const u32x4*>(kp + 16 * c) : u32x4{0, 0, 0, 0});
-      vreg[c] = as_bf16x8(ok ? *reinterpret_cast<const u32x4*>(vp + 16 * c) : u32x4{0, 0, 0, 0});
-    }
   }
-  // ---- K block transposed -> LDS (B operand of dQ = dS K) ------------------
-  for (int p = tid; p < KT_PAIRS; p += 256) {
-    const int dg = p % CPR, kg = p / CPR;
-    u32x4 in[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      int key = n0 + 4 * kg + r;
-      in[r] = key < nk ? *reinterpret_cast<const u32x4*>(kb + (long)key * D + 8 * dg)
-                       : u32x4{0, 0, 0, 0};
-    }
-    u32x2 out[8];
-    transpose4x8(in, out);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x2*>(&sm.kts[8 * dg + j][4 * kg]) = out[j];
+  // ---- the block's V rows -> LDS (B operand of dP; keeps registers free) ----
+  for (int c = tid; c < BN * CPR; c += 256) {
+    const int row = c / CPR, col = (c % CPR) * 8;
+    const int key = n0 + row;
+    *reinterpret_cast<u32x4*>(&sm.vs[row][col]) =
+        key < nk ? *reinterpret_cast<const u32x4*>(vb + (long)key * D + col) : u32x4{0, 0, 0, 0};
   }
 
   // ---- query-block walk ------------------------------------------------------
@@ -152,13 +146,11 @@ __device__ void fa2_bwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   const int st_dg = st_p % CPR, st_rg = st_p / CPR;
   u32x4 stage[4];
   float st_lse = 0.0f, st_delta = 0.0f;
+  int cur_head = 0, cur_qb = qb_first;  // (head, q-block) of the tile being staged
 
-  auto head_of = [&](int it) { return it / iters_per_head; };
-  auto qblock_of = [&](int it) { return qb_first + it % iters_per_head; };
-
-  auto load_tile = [&](int it) {
-    const long bh = (long)b * hq + (long)hk * group + head_of(it);
-    const int qb0 = qblock_of(it) * BM;
+  auto load_tile = [&]() {
+    const long bh = (long)b * hq + (long)hk * group + cur_head;
+    const int qb0 = cur_qb * BM;
     if (stager) {
       const bf16* src = st_is_do ? dout : q;
 #pragma unroll
@@ -174,11 +166,15 @@ __device__ void fa2_bwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
       st_lse = row < nq ? lse[bh * nq + row] * kLog2e : INFINITY;
       st_delta = row < nq ? delta[bh * nq + row] : 0.0f;
     }
+    if (++cur_qb == n_qb) {
+      cur_qb = qb_first;
+      ++cur_head;
+    }
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](int buf) {
     if (stager) {
-      bf16(*rm)[D + KPAD] = st_is_do ? sm.dos : sm.qs;
-      bf16(*tr)[BM + TPAD] = st_is_do ? sm.dots : sm.qts;
+      bf16(*rm)[D + KPAD] = st_is_do ? sm.dos[buf] : sm.qs[buf];
+      bf16(*tr)[BM + TPAD] = st_is_do ? sm.dots[buf] : sm.qts[buf];
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         *reinterpret_cast<u32x4*>(&rm[4 * st_rg + r][8 * st_dg]) = stage[r];
@@ -188,8 +184,8 @@ __device__ void fa2_bwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
       for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x2*>(&tr[8 * st_dg + j][4 * st_rg]) = out[j];
     }
     if (tid >= 192 && tid < 192 + BM) {
-      sm.lse2[tid - 192] = st_lse;
-      sm.delta[tid - 192] = st_delta;
+      sm.lse2[buf][tid - 192] = st_lse;
+      sm.delta[buf][tid - 192] = st_delta;
     }
   };
 
@@ -202,44 +198,47 @@ __device__ void fa2_bwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   const float sl2 = scale * kLog2e;
 
   if (n_iter > 0) {
-    load_tile(0);
-    store_tile();
+    load_tile();
+    store_tile(0);
   }
   __syncthreads();
 
+  int qb = qb_first;  // q-block of the tile in LDS
   for (int it = 0; it < n_iter; ++it) {
-    const long bh = (long)b * hq + (long)hk * group + head_of(it);
-    const int qb0 = qblock_of(it) * BM;
-    if (it + 1 < n_iter) load_tile(it + 1);
+    const int cur = 0;
+    const int qb0 = qb * BM;
+    if (++qb == n_qb) qb = qb_first;
+    if (it + 1 < n_iter) load_tile();
 
     const bool wave_active = !(CAUSAL && kw0 > qb0 + BM - 1) && kw0 < nk;
-    const bool need_mask = (kw0 + 32 > nk) || (CAUSAL && kw0 + 31 > qb0);
-    uint32_t pb[8], dsb[8];
     if (wave_active) {
+      const bool need_mask = (kw0 + 32 > nk) || (CAUSAL && kw0 + 31 > qb0);
       // S = Q K^T and dP = dO V^T, C layout: lane = key (col), 16 query rows.
       f32x16 s = f32x16{}, dp = f32x16{};
+      const bf16* qrow = &sm.qs[cur][l32][8 * g];
+      const bf16* drow = &sm.dos[cur][l32][8 * g];
+      const bf16* vrow = &sm.vs[32 * wave + l32][8 * g];
 #pragma unroll
       for (int c = 0; c < DC; ++c) {
-        u32x4 aq = *reinterpret_cast<const u32x4*>(&sm.qs[l32][16 * c + 8 * g]);
+        u32x4 aq = *reinterpret_cast<const u32x4*>(qrow + 16 * c);
         s = mfma32(as_bf16x8(aq), kreg[c], s);
+        u32x4 ad = *reinterpret_cast<const u32x4*>(drow + 16 * c);
+        u32x4 bv = *reinterpret_cast<const u32x4*>(vrow + 16 * c);
+        dp = mfma32(as_bf16x8(ad), as_bf16x8(bv), dp);
       }
-#pragma unroll
-      for (int c = 0; c < DC; ++c) {
-        u32x4 ad = *reinterpret_cast<const u32x4*>(&sm.dos[l32][16 * c + 8 * g]);
-        dp = mfma32(as_bf16x8(ad), vreg[c], dp);
-      }
+      uint32_t pb[8], dsb[8];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r0 = 8 * j + 4 * g;  // first of this register group's 4 rows
-        f32x4 l4 = *reinterpret_cast<const f32x4*>(&sm.lse2[r0]);
-        f32x4 d4 = *reinterpret_cast<const f32x4*>(&sm.delta[r0]);
+        f32x4 l4 = *reinterpret_cast<const f32x4*>(&sm.lse2[cur][r0]);
+        f32x4 d4 = *reinterpret_cast<const f32x4*>(&sm.delta[cur][r0]);
         float p[4], ds[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float pv = fast_exp2(s[4 * j + i] * sl2 - l4[i]);
+          float pv = fast_exp2(__builtin_fmaf(s[4 * j + i], sl2, -l4[i]));
           if (need_mask) {
-            int qrow = qb0 + r0 + i;
-            if (mykey >= nk || (CAUSAL && mykey > qrow)) pv = 0.0f;
+            int qrow_i = qb0 + r0 + i;
+            if (mykey >= nk || (CAUSAL && mykey > qrow_i)) pv = 0.0f;
           }
           p[i] = pv;
           ds[i] = pv * (dp[4 * j + i] - d4[i]);
@@ -257,48 +256,21 @@ __device__ void fa2_bwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
             as_bf16x8(u32x4{dsb[4 * hh], dsb[4 * hh + 1], dsb[4 * hh + 2], dsb[4 * hh + 3]});
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
-          const bf16* dor = &sm.dots[32 * t + l32][16 * hh + 4 * g];
+          const bf16* dor = &sm.dots[cur][32 * t + l32][16 * hh + 4 * g];
           u32x2 a0 = *reinterpret_cast<const u32x2*>(dor);
           u32x2 a1 = *reinterpret_cast<const u32x2*>(dor + 8);
           dv_acc[t] = mfma32(as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]}), bp, dv_acc[t]);
-          const bf16* qr = &sm.qts[32 * t + l32][16 * hh + 4 * g];
+          const bf16* qr = &sm.qts[cur][32 * t + l32][16 * hh + 4 * g];
           u32x2 c0 = *reinterpret_cast<const u32x2*>(qr);
           u32x2 c1 = *reinterpret_cast<const u32x2*>(qr + 8);
           dk_acc[t] = mfma32(as_bf16x8(u32x4{c0[0], c0[1], c1[0], c1[1]}), bs, dk_acc[t]);
         }
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) dsb[j] = 0u;
     }
-    // dS -> LDS as [query][key] for the dQ product.
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t w = dsb[2 * j + (i >> 1)];
-        uint16_t hbits = (i & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
-        reinterpret_cast<uint16_t*>(&sm.dss[8 * j + 4 * g + i][0])[32 * wave + l32] = hbits;
-      }
-    __syncthreads();
-    // dQ[32 rows, d-tile = wave] += dS[32 x 128] K[128 x 32]
-    if (wave < DT) {
-      f32x16 acc = f32x16{};
-#pragma unroll
-      for (int c = 0; c < BN / 16; ++c) {
-        u32x4 a = *reinterpret_cast<const u32x4*>(&sm.dss[l32][16 * c + 8 * g]);
-        u32x4 bk = *reinterpret_cast<const u32x4*>(&sm.kts[32 * wave + l32][16 * c + 8 * g]);
-        acc = mfma32(as_bf16x8(a), as_bf16x8(bk), acc);
-      }
-      float* dqb = dq_acc + (bh * nq) * D + 32 * wave + l32;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        int row = qb0 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (row < nq) unsafeAtomicAdd(dqb + (long)row * D, acc[r]);
-      }
+    if (it + 1 < n_iter) {
+      __syncthreads();  // every wave is done with the tile in LDS
+      store_tile(0);
     }
-    __syncthreads();
-    if (it + 1 < n_iter) store_tile();
     __syncthreads();
   }
 
@@ -321,47 +293,206 @@ __device__ void fa2_bwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   }
 }
 
-// dq = bf16(scale * dq_acc)
-__device__ void dq_convert(const float* __restrict__ acc, bf16* __restrict__ dq, float scale,
-                           long n8) {
-  long i = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n8) return;
-  float a[8];
-  f32x4 lo = *reinterpret_cast<const f32x4*>(acc + 8 * i);
-  f32x4 hi = *reinterpret_cast<const f32x4*>(acc + 8 * i + 4);
+// ===========================================================================
+// dQ (query-parallel)
+// ===========================================================================
+constexpr int QBM = 128;  // query rows per workgroup (4 waves x 32)
+constexpr int QBN = 32;   // keys per iteration
+
+template <int D>
+struct __attribute__((aligned(16))) DqSmem {
+  bf16 k[2][QBN][D + KPAD];    // K tile, row-major    (A operand of S^T)
+  bf16 v[2][QBN][D + KPAD];    // V tile, row-major    (A operand of dP^T)
+  bf16 kt[2][D][QBN + TPAD];   // K tile transposed    (A operand of dQ^T)
+};
+
+template <int D, bool CAUSAL>
+__device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                           const bf16* __restrict__ v, const bf16* __restrict__ dout,
+                           const float* __restrict__ lse, const float* __restrict__ delta,
+                           bf16* __restrict__ dq, int nq, int nk, float scale, int hq, int hkv,
+                           int num_m_blocks, int total_blocks) {
+  constexpr int DC = D / 16;
+  constexpr int DT = D / 32;
+  constexpr int CPR = D / 8;
+  constexpr int PAIRS = (QBN / 4) * CPR;  // (4-key, 8-d) blocks per tile; K and V each
+  __shared__ DqSmem<D> sm;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+
+  const int id = xcd_remap(blockIdx.x, total_blocks);
+  const int bh = id / num_m_blocks;
+  const int mb = num_m_blocks - 1 - (id - bh * num_m_blocks);
+  const int b = bh / hq, h = bh - b * hq;
+  const long kvh = (long)b * hkv + h / (hq / hkv);
+  const int m0 = mb * QBM;
+  const int qrow = m0 + wave * 32 + l32;
+  const int wave_qmax = m0 + wave * 32 + 31;
+  const bool qok = qrow < nq;
+
+  const bf16* kb = k + kvh * (long)nk * D;
+  const bf16* vb = v + kvh * (long)nk * D;
+
+  // ---- this lane's Q and dO row (B operands), LSE and Delta ----------------
+  bf16x8 qreg[DC], doreg[DC];
+  {
+    const long row = (long)bh * nq + (qok ? qrow : 0);
+    const bf16* qp = q + row * D + 8 * g;
+    const bf16* dp = dout + row * D + 8 * g;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    a[j] = lo[j] * scale;
-    a[4 + j] = hi[j] * scale;
+    for (int c = 0; c < DC; ++c) {
+      qreg[c] = as_bf16x8(qok ? *reinterpret_cast<const u32x4*>(qp + 16 * c) : u32x4{0, 0, 0, 0});
+      doreg[c] = as_bf16x8(qok ? *reinterpret_cast<const u32x4*>(dp + 16 * c) : u32x4{0, 0, 0, 0});
+    }
   }
-  Vec16<bf16>::store(dq + 8 * i, a);
+  const float lse2 = qok ? lse[(long)bh * nq + qrow] * kLog2e : INFINITY;
+  const float dlt = qok ? delta[(long)bh * nq + qrow] : 0.0f;
+  const float sl2 = scale * kLog2e;
+
+  int kend = nk;
+  if (CAUSAL) kend = min(nk, m0 + QBM);
+  const int n_iter = (kend + QBN - 1) / QBN;
+
+  // Staging: threads [0, PAIRS) carry K blocks, [PAIRS, 2*PAIRS) carry V blocks.
+  const bool stager = tid < 2 * PAIRS;
+  const bool st_is_v = tid >= PAIRS;
+  const int st_p = st_is_v ? tid - PAIRS : tid;
+  const int st_dg = st_p % CPR, st_kg = st_p / CPR;
+  u32x4 stage[4];
+  auto load_tile = [&](int kbase) {
+    if (stager) {
+      const bf16* src = st_is_v ? vb : kb;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        int key = kbase + 4 * st_kg + r;
+        stage[r] = key < nk ? *reinterpret_cast<const u32x4*>(src + (long)key * D + 8 * st_dg)
+                            : u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+    if (stager) {
+      bf16(*rm)[D + KPAD] = st_is_v ? sm.v[buf] : sm.k[buf];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<u32x4*>(&rm[4 * st_kg + r][8 * st_dg]) = stage[r];
+      if (!st_is_v) {
+        u32x2 out[8];
+        transpose4x8(stage, out);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          *reinterpret_cast<u32x2*>(&sm.kt[buf][8 * st_dg + j][4 * st_kg]) = out[j];
+      }
+    }
+  };
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
+
+  if (n_iter > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < n_iter; ++it) {
+    const int cur = it & 1;
+    const int kbase = it * QBN;
+    if (it + 1 < n_iter) load_tile(kbase + QBN);
+    if (!(CAUSAL && kbase > wave_qmax)) {
+      // S^T = K Q^T, dP^T = V dO^T: lane = query row, 16 keys.
+      f32x16 s = f32x16{}, dp = f32x16{};
+      const bf16* krow = &sm.k[cur][l32][8 * g];
+      const bf16* vrow = &sm.v[cur][l32][8 * g];
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        u32x4 ak = *reinterpret_cast<const u32x4*>(krow + 16 * c);
+        s = mfma32(as_bf16x8(ak), qreg[c], s);
+        u32x4 av = *reinterpret_cast<const u32x4*>(vrow + 16 * c);
+        dp = mfma32(as_bf16x8(av), doreg[c], dp);
+      }
+      const bool need_mask = (kbase + QBN > nk) || (CAUSAL && kbase + QBN - 1 > m0 + wave * 32);
+      uint32_t dsb[8];
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        float p0 = fast_exp2(__builtin_fmaf(s[r], sl2, -lse2));
+        float p1 = fast_exp2(__builtin_fmaf(s[r + 1], sl2, -lse2));
+        if (need_mask) {
+          int key = kbase + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (key >= nk || (CAUSAL && key > qrow)) p0 = 0.0f;
+          if (key + 1 >= nk || (CAUSAL && key + 1 > qrow)) p1 = 0.0f;
+        }
+        dsb[r >> 1] = pack_bf16x2(p0 * (dp[r] - dlt), p1 * (dp[r + 1] - dlt));
+      }
+      // dQ^T += K^T dS^T
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        bf16x8 bop =
+            as_bf16x8(u32x4{dsb[4 * hh], dsb[4 * hh + 1], dsb[4 * hh + 2], dsb[4 * hh + 3]});
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          const bf16* kr = &sm.kt[cur][32 * t + l32][16 * hh + 4 * g];
+          u32x2 a0 = *reinterpret_cast<const u32x2*>(kr);
+          u32x2 a1 = *reinterpret_cast<const u32x2*>(kr + 8);
+          acc[t] = mfma32(as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]}), bop, acc[t]);
+        }
+      }
+    }
+    if (it + 1 < n_iter) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  if (qok) {
+    bf16* dqr = dq + ((long)bh * nq + qrow) * D;
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int d = 32 * t + 8 * j + 4 * g;
+        *reinterpret_cast<u32x2*>(dqr + d) =
+            u32x2{pack_bf16x2(acc[t][4 * j] * scale, acc[t][4 * j + 1] * scale),
+                  pack_bf16x2(acc[t][4 * j + 2] * scale, acc[t][4 * j + 3] * scale)};
+      }
+  }
 }
 
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256) void teeny_fa2_bwd_dq_convert_bf16(
-    const float* acc, bf16* dq, float scale, long n8) {
-  dq_convert(acc, dq, scale, n8);
-}
-
 #define TEENY_FA2_BWD_BF16_INST(D)                                                              \
   extern "C" __global__ __launch_bounds__(256) void teeny_fa2_bwd_pre_bf16_d##D(               \
-      const bf16* o, const bf16* dout, float* delta, float* dq_acc, long rows) {               \
-    bwd_pre<D>(o, dout, delta, dq_acc, rows);                                                   \
+      const bf16* o, const bf16* dout, float* delta, long rows) {                               \
+    bwd_pre<D>(o, dout, delta, rows);                                                           \
   }                                                                                             \
-  extern "C" __global__ __launch_bounds__(256) void teeny_fa2_bwd_bf16_d##D##_c(               \
+  extern "C" __global__ __launch_bounds__(256) void teeny_fa2_bwd_dkdv_bf16_d##D##_c(          \
       const bf16* q, const bf16* k, const bf16* v, const bf16* dout, const float* lse,          \
-      const float* delta, float* dq_acc, bf16* dk, bf16* dv, int nq, int nk, float scale,       \
-      int hq, int hkv, int nnb, int total) {                                                    \
-    fa2_bwd_bf16<D, true>(q, k, v, dout, lse, delta, dq_acc, dk, dv, nq, nk, scale, hq, hkv,   \
-                          nnb, total);                                                          \
+      const float* delta, bf16* dk, bf16* dv, int nq, int nk, float scale, int hq, int hkv,     \
+      int nnb, int total) {                                                                     \
+    fa2_bwd_dkdv<D, true>(q, k, v, dout, lse, delta, dk, dv, nq, nk, scale, hq, hkv, nnb,      \
+                          total);                                                               \
   }                                                                                             \
-  extern "C" __global__ __launch_bounds__(256) void teeny_fa2_bwd_bf16_d##D##_n(               \
+  extern "C" __global__ __launch_bounds__(256) void teeny_fa2_bwd_dkdv_bf16_d##D##_n(          \
       const bf16* q, const bf16* k, const bf16* v, const bf16* dout, const float* lse,          \
-      const float* delta, float* dq_acc, bf16* dk, bf16* dv, int nq, int nk, float scale,       \
-      int hq, int hkv, int nnb, int total) {                                                    \
-    fa2_bwd_bf16<D, false>(q, k, v, dout, lse, delta, dq_acc, dk, dv, nq, nk, scale, hq, hkv,  \
-                           nnb, total);                                                         \
+      const float* delta, bf16* dk, bf16* dv, int nq, int nk, float scale, int hq, int hkv,     \
+      int nnb, int total) {                                                                     \
+    fa2_bwd_dkdv<D, false>(q, k, v, dout, lse, delta, dk, dv, nq, nk, scale, hq, hkv, nnb,     \
+                           total);                                                              \
+  }                                                                                             \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
+  void teeny_fa2_bwd_dq_bf16_d##D##_c(const bf16* q, const bf16* k, const bf16* v,             \
+                                      const bf16* dout, const float* lse, const float* delta,   \
+                                      bf16* dq, int nq, int nk, float scale, int hq, int hkv,   \
+                                      int nmb, int total) {                                     \
+    fa2_bwd_dq<D, true>(q, k, v, dout, lse, delta, dq, nq, nk, scale, hq, hkv, nmb, total);    \
+  }                                                                                             \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
+  void teeny_fa2_bwd_dq_bf16_d##D##_n(const bf16* q, const bf16* k, const bf16* v,             \
+                                      const bf16* dout, const float* lse, const float* delta,   \
+                                      bf16* dq, int nq, int nk, float scale, int hq, int hkv,   \
+                                      int nmb, int total) {                                     \
+    fa2_bwd_dq<D, false>(q, k, v, dout, lse, delta, dq, nq, nk, scale, hq, hkv, nmb, total);   \
   }
 
 TEENY_FA2_BWD_BF16_INST(64)

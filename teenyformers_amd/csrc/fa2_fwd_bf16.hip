@@ -35,6 +35,7 @@ constexpr int KPAD = 8;  // K tile row padding (elements)
 constexpr int VPAD = 4;  // Vt tile row padding (elements)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kRescale = 8.0f;  // lazy-rescale threshold, log2 units
 
 DEVI float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -45,7 +46,7 @@ DEVI f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 }
 
 template <int D>
-struct FwdSmem {
+struct __attribute__((aligned(16))) FwdSmem {
   bf16 k[2][BN][D + KPAD];
   bf16 vt[2][D][BN + VPAD];
 };
@@ -143,8 +144,12 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   f32x16 acc_o[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc_o[t] = f32x16{};
-  float m_run = -INFINITY;  // running max, log2 domain
-  float l_run = 0.0f;       // this lane's partial row sum (its 16 of every 32 keys)
+  // m_run: the reference max of this lane's query row in log2 units.  It is
+  // raised lazily: only when some row of the wave sees a max more than
+  // kRescale above its m_run are O and l rescaled, so p = 2^(t - m_run) stays
+  // below 2^kRescale (exact in fp32 and representable in bf16).
+  float m_run = -INFINITY;
+  float l_run = 0.0f;  // this lane's partial row sum (its 16 of every 32 keys)
   const float sl2 = scale * kLog2e;
 
   if (n_iter > 0) {
@@ -157,65 +162,77 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
     const int cur = it & 1;
     const int kbase = it * BN;
     if (it + 1 < n_iter) load_tile(kbase + BN);
+    // causal: a tile whose first key is past this wave's last row is all masked
+    const bool act0 = !(CAUSAL && kbase > wave_qmax);
+    if (act0) {
 
-    // ---- S^T = K Q^T for the two 32-key subtiles ----
-    f32x16 s[2];
-    bool act[2];
+    // ---- S^T = K Q^T for the two 32-key subtiles (chains interleaved) ----
+    const bool act1 = kbase + 32 < nk && !(CAUSAL && kbase + 32 > wave_qmax);
+    f32x16 s0 = f32x16{}, s1 = f32x16{};
+    {
+      const bf16* k0 = &sm.k[cur][l32][8 * g];
+      const bf16* k1 = &sm.k[cur][32 + l32][8 * g];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const int key0 = kbase + 32 * kt;
-      act[kt] = key0 < nk && !(CAUSAL && key0 > wave_qmax);
-      s[kt] = f32x16{};
-      if (act[kt]) {
-#pragma unroll
-        for (int c = 0; c < DC; ++c) {
-          u32x4 a = *reinterpret_cast<const u32x4*>(&sm.k[cur][32 * kt + l32][16 * c + 8 * g]);
-          s[kt] = mfma32(as_bf16x8(a), qreg[c], s[kt]);
+      for (int c = 0; c < DC; ++c) {
+        u32x4 a0 = *reinterpret_cast<const u32x4*>(k0 + 16 * c);
+        s0 = mfma32(as_bf16x8(a0), qreg[c], s0);
+        if (act1) {
+          u32x4 a1 = *reinterpret_cast<const u32x4*>(k1 + 16 * c);
+          s1 = mfma32(as_bf16x8(a1), qreg[c], s1);
         }
       }
     }
 
-    // ---- online softmax (log2 domain) ----
+    // ---- masking (boundary tiles only): raw scores -> -inf ----
     const bool need_mask = (kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > m0 + wave * 32);
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+    if (need_mask) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float t = act[kt] ? s[kt][r] * sl2 : -INFINITY;
-        if (need_mask) {
-          int key = kbase + 32 * kt + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key >= nk || (CAUSAL && key > qrow)) t = -INFINITY;
-        }
-        s[kt][r] = t;
-        mx = fmaxf(mx, t);
+        int key = kbase + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (key >= nk || (CAUSAL && key > qrow)) s0[r] = -INFINITY;
+        key += 32;
+        if (!act1 || key >= nk || (CAUSAL && key > qrow)) s1[r] = -INFINITY;
       }
+    } else if (!act1) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s1[r] = -INFINITY;
     }
+
+    // ---- online softmax, log2 domain, lazy rescale ----
+    float mx = fmaxf(s0[0], s1[0]);
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = fast_exp2(m_run - m_use);
-    m_run = m_new;
+    const float m_tile = mx * sl2;  // scale > 0, so max(scale*s) = scale*max(s)
+    const bool grow = m_tile > m_run + kRescale;
+    if (__any(grow)) {
+      const float m_new = fmaxf(m_run, m_tile);
+      // 0 on a row's first tile; 1 for rows that did not grow (or saw no key)
+      const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) acc_o[t] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
     float psum = 0.0f;
     uint32_t pb[2][8];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        float p0 = fast_exp2(s[kt][r] - m_use);
-        float p1 = fast_exp2(s[kt][r + 1] - m_use);
-        psum += p0 + p1;
-        pb[kt][r >> 1] = pack_bf16x2(p0, p1);
-      }
+    for (int r = 0; r < 16; r += 2) {
+      float p0 = fast_exp2(__builtin_fmaf(s0[r], sl2, -m_use));
+      float p1 = fast_exp2(__builtin_fmaf(s0[r + 1], sl2, -m_use));
+      float p2 = fast_exp2(__builtin_fmaf(s1[r], sl2, -m_use));
+      float p3 = fast_exp2(__builtin_fmaf(s1[r + 1], sl2, -m_use));
+      psum += (p0 + p1) + (p2 + p3);
+      pb[0][r >> 1] = pack_bf16x2(p0, p1);
+      pb[1][r >> 1] = pack_bf16x2(p2, p3);
     }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int t = 0; t < DT; ++t) acc_o[t] *= alpha;
+    l_run += psum;
 
     // ---- O^T += V^T P^T ----
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
-      if (!act[kt]) continue;
+      if (kt == 1 && !act1) break;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         bf16x8 bop = as_bf16x8(u32x4{pb[kt][4 * hh], pb[kt][4 * hh + 1], pb[kt][4 * hh + 2],
@@ -229,6 +246,7 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
         }
       }
     }
+    }  // act0
 
     if (it + 1 < n_iter) store_tile(cur ^ 1);
     __syncthreads();
@@ -256,12 +274,14 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
 }  // namespace
 
 #define TEENY_FA2_FWD_BF16_INST(D)                                                               \
-  extern "C" __global__ __launch_bounds__(256) void teeny_fa2_fwd_bf16_d##D##_c(               \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
+  void teeny_fa2_fwd_bf16_d##D##_c(                                                              \
       const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,            \
       float scale, int hq, int hkv, int nmb, int total) {                                        \
     fa2_fwd_bf16<D, true>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);                    \
   }                                                                                              \
-  extern "C" __global__ __launch_bounds__(256) void teeny_fa2_fwd_bf16_d##D##_n(               \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
+  void teeny_fa2_fwd_bf16_d##D##_n(                                                              \
       const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,            \
       float scale, int hq, int hkv, int nmb, int total) {                                        \
     fa2_fwd_bf16<D, false>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);                   \

@@ -55,7 +55,7 @@ def test_fa2_fwd_validation(L):
 def test_fa2_bwd_workspace(L):
     need = L.teeny_flash_attn2_bwd_workspace_bytes(4096, 8, 32, 128, BF16)
     rows = 8 * 32 * 4096
-    assert need >= rows * 4 + rows * 128 * 4
+    assert need >= rows * 4  # Delta
     assert L.teeny_flash_attn2_bwd_workspace_bytes(128, 1, 4, 64, F32) >= 4 * 128 * 4
     small = L.teeny_flash_attn2_bwd_workspace_bytes(128, 1, 4, 64, BF16)
     rc = L.teeny_causal_flash_attn2_bwd(P, P, P, P, P, P, P, P, P, 128, 128, 0.125, 1, 4, 4, 64,
