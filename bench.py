@@ -6,7 +6,9 @@ are resident in HBM before timing.  Prints one JSON line:
   value       whole-step throughput in TFLOP/s (algorithmic: causal forward
               4*B*H*S^2*D/2, backward 2.5x that)
   roofline    the dominant kernel (most summed time) measured with HIP events
-              recorded on its launch stream during the timed steps
+              recorded on its launch stream during the timed steps; traffic =
+              that kernel's HBM bytes per launch from the committed rocprofv3
+              FETCH_SIZE / WRITE_SIZE summary (profiles/*_hbm_traffic.md)
   cpu_baseline the oracle's restatement of the reference kernels (fp32,
               every key of every row, as the reference loops) timed on a
               sample of heads on this host's cores
@@ -43,8 +45,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=4,
+    ap.add_argument("--cpu-heads", type=int, default=48,
                     help="heads of the workload the CPU baseline times")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="after the timed steps, run one head transpose (a pure copy) of "
+                         "Q's 256 MiB, the known-size reference for HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -86,6 +91,10 @@ def main() -> int:
     elapsed = time.perf_counter() - t0
     _lib.profile_enable(False)
     stats = _lib.profile_stats()
+    if args.calibrate_copy:
+        # [B, S, H*D] -> [B, H, S, D]: reads and writes q.numel() * 2 bytes
+        ops.transpose_heads(q.view(B, S, H * D), H)
+        torch.cuda.synchronize()
 
     f_fwd = fwd_flops(B, H, S, S, D)
     f_bwd = 2.5 * f_fwd
@@ -131,7 +140,7 @@ def main() -> int:
         "roofline": {"bound": "mfma", "kernel": dominant,
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": traffic_from_profiles(dominant)},
         "cpu_baseline": None,
         "detail": {
             "pct_mfma_peak_step": round(value / PEAK_BF16_TFLOPS, 4),
@@ -149,6 +158,20 @@ def main() -> int:
         out["cpu_baseline"] = cpu_baseline(q, k, v, do, scale, args.cpu_heads)
     print(json.dumps(out), flush=True)
     return 0
+
+
+def traffic_from_profiles(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summaries."""
+    import glob
+    import re
+
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_hbm_traffic.md"))):
+        with open(path) as f:
+            for line in f:
+                m = re.match(r"- traffic_bytes_per_launch (\S+) (\S+)", line.strip())
+                if m and m.group(1) == kernel:
+                    return float(m.group(2))
+    return None
 
 
 def cpu_baseline(q, k, v, do, scale, n_heads):
