@@ -12,12 +12,13 @@
 //   2. dK/dV, key-parallel: one workgroup (4 wavefronts) owns 128 keys of one
 //      (b, kv head); each wave's 32 K rows stay in registers and its V rows in
 //      LDS as B operands of v_mfma_f32_32x32x16_bf16, and it walks the 32-row query
-//      blocks of every q head of its GQA group (Q, dO staged in LDS row-major
-//      and transposed), accumulating dK^T and dV^T in registers: the GQA
-//      reduction comes for free;
+//      blocks of every q head of its GQA group (Q, dO staged row-major in
+//      double-buffered LDS and read both row-wise and, through the LDS
+//      transpose read, as Q^T / dO^T), accumulating dK^T and dV^T in
+//      registers: the GQA reduction comes for free;
 //   3. dQ, query-parallel, shaped like the forward: each wave's Q and dO
-//      rows are B operands in registers, 32-key tiles of K, V (row-major) and
-//      K^T stream through double-buffered LDS, S^T and dP^T put one query row
+//      rows are B operands in registers, 32-key tiles of K and V stream
+//      through double-buffered LDS (K^T via the transpose read), S^T and dP^T put one query row
 //      in each lane, and dQ^T += K^T dS^T accumulates in registers.
 // Recomputing S and dP in the dQ kernel costs 7 matrix products per tile
 // pair instead of 5; in exchange neither kernel needs dS round trips through
@@ -30,8 +31,8 @@ namespace {
 
 constexpr int BN = 128;  // keys per workgroup
 constexpr int BM = 32;   // query rows per iteration
-constexpr int KPAD = 8;
-constexpr int TPAD = 4;
+constexpr int KPAD = 8;   // rows read only row-wise: stride = 4 mod 64 dwords
+constexpr int QPAD = 24;  // rows read row-wise and transposed: stride = 12 mod 64 dwords (D=128)
 constexpr float kLog2e = 1.4426950408889634f;
 
 DEVI float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -40,16 +41,31 @@ DEVI f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// 4 rows x 8 columns (row-major, 4 x 16 bytes) -> 8 rows x 4 columns
-// (8 x 8 bytes) of 16-bit elements.  out[j] is column j as (r0,r1 | r2,r3).
-DEVI void transpose4x8(const u32x4 (&in)[4], u32x2 (&out)[8]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    out[2 * j] = u32x2{__builtin_amdgcn_perm(in[1][j], in[0][j], 0x05040100u),
-                       __builtin_amdgcn_perm(in[3][j], in[2][j], 0x05040100u)};
-    out[2 * j + 1] = u32x2{__builtin_amdgcn_perm(in[1][j], in[0][j], 0x07060302u),
-                           __builtin_amdgcn_perm(in[3][j], in[2][j], 0x07060302u)};
-  }
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, output lane i receives
+// element (i % 4) of the 8-byte chunks addressed by lanes i/4, i/4+4, i/4+8
+// and i/4+12 (measured on gfx950): lanes addressing a 4-row x 16-column block
+// of a row-major tile receive it transposed, one column per lane.
+DEVI u32x2 lds_read_tr(const bf16* p) {
+  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// A operand X^T of v_mfma_f32_32x32x16_bf16 (M = columns of X, K = rows of
+// X) from a row-major LDS tile X whose rows hold the summation index:
+// lane (l32, g) receives X[r0 + 4g + 0..3][c0 + l32] and
+// X[r0 + 8 + 4g + 0..3][c0 + l32], the row order in which a 32x32 MFMA
+// accumulator holds rows 16hh + 8*(e/4) + 4g + e%4 for its B operand.
+template <int STRIDE>
+DEVI bf16x8 xt_operand(const bf16* tile, int r0, int c0, int lane) {
+  const int g = lane >> 5;
+  const bf16* p = tile + (r0 + 4 * g + ((lane & 15) >> 2)) * STRIDE + c0 +
+                  16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  u32x2 a0 = lds_read_tr(p);
+  u32x2 a1 = lds_read_tr(p + 8 * STRIDE);
+  return as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
 }
 
 // Delta = rowsum(O o dO) in fp32.
@@ -75,17 +91,13 @@ __device__ void bwd_pre(const bf16* __restrict__ o, const bf16* __restrict__ dou
 // ===========================================================================
 // dK / dV (key-parallel)
 // ===========================================================================
-// One buffer of Q / dO tiles (the next tile waits in registers) so that two
-// workgroups fit in a CU's LDS.
 template <int D>
 struct __attribute__((aligned(16))) DkdvSmem {
-  bf16 qs[1][BM][D + KPAD];    // Q tile, row-major  (A operand of S)
-  bf16 dos[1][BM][D + KPAD];   // dO tile, row-major (A operand of dP)
-  bf16 qts[1][D][BM + TPAD];   // Q tile transposed  (A operand of dK^T)
-  bf16 dots[1][D][BM + TPAD];  // dO tile transposed (A operand of dV^T)
-  float lse2[1][BM];           // LSE * log2(e); +inf for rows past nq
-  float delta[1][BM];
-  bf16 vs[BN][D + KPAD];       // the block's V rows (B operand of dP)
+  bf16 qs[2][BM][D + QPAD];   // Q tile: A operand of S, transposed A operand of dK^T
+  bf16 dos[2][BM][D + QPAD];  // dO tile: A operand of dP, transposed A operand of dV^T
+  float lse2[2][BM];          // LSE * log2(e); +inf for rows past nq
+  float delta[2][BM];
+  bf16 vs[BN][D + KPAD];      // the block's V rows (B operand of dP)
 };
 
 template <int D, bool CAUSAL>
@@ -97,7 +109,6 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
   constexpr int DC = D / 16;  // d-chunks of 16 (QK^T, dO V^T)
   constexpr int DT = D / 32;  // d-tiles of 32 (dK^T, dV^T)
   constexpr int CPR = D / 8;  // 16-byte chunks per row
-  constexpr int TILE_PAIRS = (BM / 4) * CPR;  // (4-row, 8-col) blocks per Q (or dO) tile
   __shared__ DkdvSmem<D> sm;
 
   const int tid = threadIdx.x;
@@ -139,27 +150,23 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
   const int iters_per_head = n_qb > qb_first ? n_qb - qb_first : 0;
   const int n_iter = group * iters_per_head;
 
-  // Staging: threads [0, TILE_PAIRS) carry Q, [TILE_PAIRS, 2*TILE_PAIRS) carry dO.
-  const bool stager = tid < 2 * TILE_PAIRS;
-  const bool st_is_do = tid >= TILE_PAIRS;
-  const int st_p = st_is_do ? tid - TILE_PAIRS : tid;
-  const int st_dg = st_p % CPR, st_rg = st_p / CPR;
-  u32x4 stage[4];
+  // Staging: a Q or dO tile is BM x CPR 16-byte chunks; each thread carries
+  // TCH chunks of both.
+  constexpr int TCH = BM * CPR / 256;
+  u32x4 qstage[TCH], dstage[TCH];
   float st_lse = 0.0f, st_delta = 0.0f;
   int cur_head = 0, cur_qb = qb_first;  // (head, q-block) of the tile being staged
 
   auto load_tile = [&]() {
     const long bh = (long)b * hq + (long)hk * group + cur_head;
     const int qb0 = cur_qb * BM;
-    if (stager) {
-      const bf16* src = st_is_do ? dout : q;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int row = qb0 + 4 * st_rg + r;
-        stage[r] = row < nq
-                       ? *reinterpret_cast<const u32x4*>(src + (bh * nq + row) * D + 8 * st_dg)
-                       : u32x4{0, 0, 0, 0};
-      }
+    for (int i = 0; i < TCH; ++i) {
+      const int c = i * 256 + tid;
+      const int row = qb0 + c / CPR;
+      const long off = (bh * nq + row) * D + (c % CPR) * 8;
+      qstage[i] = row < nq ? *reinterpret_cast<const u32x4*>(q + off) : u32x4{0, 0, 0, 0};
+      dstage[i] = row < nq ? *reinterpret_cast<const u32x4*>(dout + off) : u32x4{0, 0, 0, 0};
     }
     if (tid >= 192 && tid < 192 + BM) {
       int row = qb0 + (tid - 192);
@@ -172,16 +179,11 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
     }
   };
   auto store_tile = [&](int buf) {
-    if (stager) {
-      bf16(*rm)[D + KPAD] = st_is_do ? sm.dos[buf] : sm.qs[buf];
-      bf16(*tr)[BM + TPAD] = st_is_do ? sm.dots[buf] : sm.qts[buf];
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        *reinterpret_cast<u32x4*>(&rm[4 * st_rg + r][8 * st_dg]) = stage[r];
-      u32x2 out[8];
-      transpose4x8(stage, out);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x2*>(&tr[8 * st_dg + j][4 * st_rg]) = out[j];
+    for (int i = 0; i < TCH; ++i) {
+      const int c = i * 256 + tid;
+      *reinterpret_cast<u32x4*>(&sm.qs[buf][c / CPR][(c % CPR) * 8]) = qstage[i];
+      *reinterpret_cast<u32x4*>(&sm.dos[buf][c / CPR][(c % CPR) * 8]) = dstage[i];
     }
     if (tid >= 192 && tid < 192 + BM) {
       sm.lse2[buf][tid - 192] = st_lse;
@@ -203,9 +205,9 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
   }
   __syncthreads();
 
-  int qb = qb_first;  // q-block of the tile in LDS
+  int qb = qb_first;  // q-block of the tile in LDS buffer `cur`
   for (int it = 0; it < n_iter; ++it) {
-    const int cur = 0;
+    const int cur = it & 1;
     const int qb0 = qb * BM;
     if (++qb == n_qb) qb = qb_first;
     if (it + 1 < n_iter) load_tile();
@@ -256,21 +258,14 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
             as_bf16x8(u32x4{dsb[4 * hh], dsb[4 * hh + 1], dsb[4 * hh + 2], dsb[4 * hh + 3]});
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
-          const bf16* dor = &sm.dots[cur][32 * t + l32][16 * hh + 4 * g];
-          u32x2 a0 = *reinterpret_cast<const u32x2*>(dor);
-          u32x2 a1 = *reinterpret_cast<const u32x2*>(dor + 8);
-          dv_acc[t] = mfma32(as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]}), bp, dv_acc[t]);
-          const bf16* qr = &sm.qts[cur][32 * t + l32][16 * hh + 4 * g];
-          u32x2 c0 = *reinterpret_cast<const u32x2*>(qr);
-          u32x2 c1 = *reinterpret_cast<const u32x2*>(qr + 8);
-          dk_acc[t] = mfma32(as_bf16x8(u32x4{c0[0], c0[1], c1[0], c1[1]}), bs, dk_acc[t]);
+          dv_acc[t] = mfma32(xt_operand<D + QPAD>(&sm.dos[cur][0][0], 16 * hh, 32 * t, lane), bp,
+                             dv_acc[t]);
+          dk_acc[t] = mfma32(xt_operand<D + QPAD>(&sm.qs[cur][0][0], 16 * hh, 32 * t, lane), bs,
+                             dk_acc[t]);
         }
       }
     }
-    if (it + 1 < n_iter) {
-      __syncthreads();  // every wave is done with the tile in LDS
-      store_tile(0);
-    }
+    if (it + 1 < n_iter) store_tile(cur ^ 1);
     __syncthreads();
   }
 
@@ -301,9 +296,8 @@ constexpr int QBN = 32;   // keys per iteration
 
 template <int D>
 struct __attribute__((aligned(16))) DqSmem {
-  bf16 k[2][QBN][D + KPAD];    // K tile, row-major    (A operand of S^T)
-  bf16 v[2][QBN][D + KPAD];    // V tile, row-major    (A operand of dP^T)
-  bf16 kt[2][D][QBN + TPAD];   // K tile transposed    (A operand of dQ^T)
+  bf16 k[2][QBN][D + QPAD];  // K tile: A operand of S^T, transposed A operand of dQ^T
+  bf16 v[2][QBN][D + KPAD];  // V tile: A operand of dP^T
 };
 
 template <int D, bool CAUSAL>
@@ -315,7 +309,6 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   constexpr int DC = D / 16;
   constexpr int DT = D / 32;
   constexpr int CPR = D / 8;
-  constexpr int PAIRS = (QBN / 4) * CPR;  // (4-key, 8-d) blocks per tile; K and V each
   __shared__ DqSmem<D> sm;
 
   const int tid = threadIdx.x;
@@ -355,36 +348,26 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   if (CAUSAL) kend = min(nk, m0 + QBM);
   const int n_iter = (kend + QBN - 1) / QBN;
 
-  // Staging: threads [0, PAIRS) carry K blocks, [PAIRS, 2*PAIRS) carry V blocks.
-  const bool stager = tid < 2 * PAIRS;
-  const bool st_is_v = tid >= PAIRS;
-  const int st_p = st_is_v ? tid - PAIRS : tid;
-  const int st_dg = st_p % CPR, st_kg = st_p / CPR;
-  u32x4 stage[4];
+  // Staging: a K or V tile is QBN x CPR 16-byte chunks; each thread carries
+  // TCH chunks of both.
+  constexpr int TCH = QBN * CPR / 256;
+  u32x4 kstage[TCH], vstage[TCH];
   auto load_tile = [&](int kbase) {
-    if (stager) {
-      const bf16* src = st_is_v ? vb : kb;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int key = kbase + 4 * st_kg + r;
-        stage[r] = key < nk ? *reinterpret_cast<const u32x4*>(src + (long)key * D + 8 * st_dg)
-                            : u32x4{0, 0, 0, 0};
-      }
+    for (int i = 0; i < TCH; ++i) {
+      const int c = i * 256 + tid;
+      const int key = kbase + c / CPR;
+      const long off = (long)key * D + (c % CPR) * 8;
+      kstage[i] = key < nk ? *reinterpret_cast<const u32x4*>(kb + off) : u32x4{0, 0, 0, 0};
+      vstage[i] = key < nk ? *reinterpret_cast<const u32x4*>(vb + off) : u32x4{0, 0, 0, 0};
     }
   };
   auto store_tile = [&](int buf) {
-    if (stager) {
-      bf16(*rm)[D + KPAD] = st_is_v ? sm.v[buf] : sm.k[buf];
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        *reinterpret_cast<u32x4*>(&rm[4 * st_kg + r][8 * st_dg]) = stage[r];
-      if (!st_is_v) {
-        u32x2 out[8];
-        transpose4x8(stage, out);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          *reinterpret_cast<u32x2*>(&sm.kt[buf][8 * st_dg + j][4 * st_kg]) = out[j];
-      }
+    for (int i = 0; i < TCH; ++i) {
+      const int c = i * 256 + tid;
+      *reinterpret_cast<u32x4*>(&sm.k[buf][c / CPR][(c % CPR) * 8]) = kstage[i];
+      *reinterpret_cast<u32x4*>(&sm.v[buf][c / CPR][(c % CPR) * 8]) = vstage[i];
     }
   };
 
@@ -433,12 +416,9 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
         bf16x8 bop =
             as_bf16x8(u32x4{dsb[4 * hh], dsb[4 * hh + 1], dsb[4 * hh + 2], dsb[4 * hh + 3]});
 #pragma unroll
-        for (int t = 0; t < DT; ++t) {
-          const bf16* kr = &sm.kt[cur][32 * t + l32][16 * hh + 4 * g];
-          u32x2 a0 = *reinterpret_cast<const u32x2*>(kr);
-          u32x2 a1 = *reinterpret_cast<const u32x2*>(kr + 8);
-          acc[t] = mfma32(as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]}), bop, acc[t]);
-        }
+        for (int t = 0; t < DT; ++t)
+          acc[t] = mfma32(xt_operand<D + QPAD>(&sm.k[cur][0][0], 16 * hh, 32 * t, lane), bop,
+                          acc[t]);
       }
     }
     if (it + 1 < n_iter) store_tile(cur ^ 1);

@@ -10,9 +10,9 @@
 // Tiling (one workgroup = 4 wavefronts = 128 query rows of one (b, h)):
 //   * each wave owns 32 query rows; its Q rows live in registers as the
 //     B operand of v_mfma_f32_32x32x16_bf16;
-//   * K/V advance in tiles of 64 keys, double-buffered in LDS; K is stored
-//     row-major [key][d] (A operand, 16-byte reads), V is transposed on its
-//     way into LDS as Vt[d][key] so the PV product reads it as an A operand;
+//   * K/V advance in tiles of 64 keys, double-buffered in LDS, both stored
+//     row-major [key][d]; K is read as an A operand with 16-byte reads, V^T
+//     with the LDS transpose read ds_read_b64_tr_b16 (see vt_operand);
 //   * S^T = K Q^T puts one query row in each lane (lane % 32) and 16 keys per
 //     lane per 32-key subtile, so the row max / row sum are in-lane plus one
 //     exchange between the two lane halves;
@@ -31,8 +31,8 @@ namespace {
 
 constexpr int BM = 128;  // query rows per workgroup
 constexpr int BN = 64;   // keys per iteration
-constexpr int KPAD = 8;  // K tile row padding (elements)
-constexpr int VPAD = 4;  // Vt tile row padding (elements)
+constexpr int KPAD = 8;   // K row padding: row stride = 4 mod 64 dwords (16-byte reads)
+constexpr int VPAD = 32;  // V row padding: row stride = 16 mod 64 dwords (transpose reads)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescale = 8.0f;  // lazy-rescale threshold, log2 units
@@ -48,8 +48,21 @@ DEVI f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 template <int D>
 struct __attribute__((aligned(16))) FwdSmem {
   bf16 k[2][BN][D + KPAD];
-  bf16 vt[2][D][BN + VPAD];
+  bf16 v[2][BN][D + VPAD];
 };
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, output lane i receives
+// element (i % 4) of the 8-byte chunks addressed by lanes i/4, i/4+4, i/4+8
+// and i/4+12 (measured on gfx950).  So if lane p of the group addresses row
+// r0 + p/4, columns c0 + 4*(p%4) .. +3 of a row-major tile, lane i receives
+// column c0 + i of rows r0 .. r0+3: a 4 x 16 block read transposed.
+DEVI u32x2 lds_read_tr(const bf16* p) {
+  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
 
 template <int D, bool CAUSAL>
 __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict__ k,
@@ -59,8 +72,7 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   constexpr int DC = D / 16;              // d-chunks of 16 for QK^T
   constexpr int DT = D / 32;              // d-tiles of 32 for PV
   constexpr int CPR = D / 8;              // 16-byte chunks per K row
-  constexpr int KCH = BN * CPR / 256;     // K chunks per thread
-  constexpr int VPAIRS = (BN / 4) * CPR;  // (4-key group, 8-d group) pairs
+  constexpr int KCH = BN * CPR / 256;     // K (and V) chunks per thread
   __shared__ FwdSmem<D> sm;
 
   const int tid = threadIdx.x;
@@ -95,25 +107,25 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   if (CAUSAL) kend = min(nk, m0 + BM);
   const int n_iter = (kend + BN - 1) / BN;
 
-  // ---- global -> register staging of one K/V tile --------------------------
-  u32x4 kstage[KCH];
-  u32x4 vstage[4];
-  const int v_dg = tid % CPR, v_kg = tid / CPR;  // valid when tid < VPAIRS
+  // ---- global -> register staging of one K/V tile (row-major 16-byte chunks)
+  u32x4 kstage[KCH], vstage[KCH];
   auto load_tile = [&](int kbase) {
+    if (kbase + BN <= nk) {  // interior tile: no bounds checks
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      int c = i * 256 + tid;
-      int row = c / CPR, col = (c % CPR) * 8;
-      int key = kbase + row;
-      kstage[i] = key < nk ? *reinterpret_cast<const u32x4*>(kb + (long)key * D + col)
-                           : u32x4{0, 0, 0, 0};
-    }
-    if (tid < VPAIRS) {
+      for (int i = 0; i < KCH; ++i) {
+        int c = i * 256 + tid;
+        long off = (long)(kbase + c / CPR) * D + (c % CPR) * 8;
+        kstage[i] = *reinterpret_cast<const u32x4*>(kb + off);
+        vstage[i] = *reinterpret_cast<const u32x4*>(vb + off);
+      }
+    } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int key = kbase + 4 * v_kg + r;
-        vstage[r] = key < nk ? *reinterpret_cast<const u32x4*>(vb + (long)key * D + 8 * v_dg)
-                             : u32x4{0, 0, 0, 0};
+      for (int i = 0; i < KCH; ++i) {
+        int c = i * 256 + tid;
+        int key = kbase + c / CPR;
+        long off = (long)key * D + (c % CPR) * 8;
+        kstage[i] = key < nk ? *reinterpret_cast<const u32x4*>(kb + off) : u32x4{0, 0, 0, 0};
+        vstage[i] = key < nk ? *reinterpret_cast<const u32x4*>(vb + off) : u32x4{0, 0, 0, 0};
       }
     }
   };
@@ -123,22 +135,15 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
       int c = i * 256 + tid;
       int row = c / CPR, col = (c % CPR) * 8;
       *reinterpret_cast<u32x4*>(&sm.k[buf][row][col]) = kstage[i];
-    }
-    if (tid < VPAIRS) {
-      // 4 keys x 8 d (row-major in vstage) -> 8 d-rows x 4 keys in Vt.
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        // d = 8*dg + 2j (low halves) and 8*dg + 2j + 1 (high halves)
-        uint32_t k01_lo = __builtin_amdgcn_perm(vstage[1][j], vstage[0][j], 0x05040100u);
-        uint32_t k23_lo = __builtin_amdgcn_perm(vstage[3][j], vstage[2][j], 0x05040100u);
-        uint32_t k01_hi = __builtin_amdgcn_perm(vstage[1][j], vstage[0][j], 0x07060302u);
-        uint32_t k23_hi = __builtin_amdgcn_perm(vstage[3][j], vstage[2][j], 0x07060302u);
-        *reinterpret_cast<u32x2*>(&sm.vt[buf][8 * v_dg + 2 * j][4 * v_kg]) = u32x2{k01_lo, k23_lo};
-        *reinterpret_cast<u32x2*>(&sm.vt[buf][8 * v_dg + 2 * j + 1][4 * v_kg]) =
-            u32x2{k01_hi, k23_hi};
-      }
+      *reinterpret_cast<u32x4*>(&sm.v[buf][row][col]) = vstage[i];
     }
   };
+  // V^T operand addressing (lds_read_tr): lane p of 16-lane group G reads
+  // row 4*g + p/4 (+8 for the second half), columns 16*(G%2) + 4*(p%4), so
+  // lane (l32, g) receives V[key][32t + l32] for the keys 16hh + 4g + 0..3
+  // and 16hh + 8 + 4g + 0..3: the order the P^T accumulator holds them in.
+  const int tr_row = 4 * g + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   // ---- running state ---------------------------------------------------------
   f32x16 acc_o[DT];
@@ -239,9 +244,9 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
                                      pb[kt][4 * hh + 3]});
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
-          const bf16* vrow = &sm.vt[cur][32 * t + l32][32 * kt + 16 * hh + 4 * g];
-          u32x2 a0 = *reinterpret_cast<const u32x2*>(vrow);
-          u32x2 a1 = *reinterpret_cast<const u32x2*>(vrow + 8);
+          const bf16* vp = &sm.v[cur][32 * kt + 16 * hh + tr_row][32 * t + tr_col];
+          u32x2 a0 = lds_read_tr(vp);
+          u32x2 a1 = lds_read_tr(vp + 8 * (D + VPAD));
           acc_o[t] = mfma32(as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]}), bop, acc_o[t]);
         }
       }
