@@ -61,10 +61,15 @@ def _run(cmd, verbose):
     return r
 
 
+# Per-file additions (none at present).
+EXTRA_FLAGS: dict[str, list[str]] = {}
+
+
 def _hipcc(name, verbose):
     src = os.path.join(CSRC, name + ".hip")
     out = os.path.join(BUILD, name + ".hsaco")
-    cmd = [os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, "-I", CSRC, src, "-o", out]
+    cmd = [os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, *EXTRA_FLAGS.get(name, []),
+           "-I", CSRC, src, "-o", out]
     _run(cmd, verbose)
     return out
 
