@@ -198,6 +198,32 @@ int teeny_token_embed_fwd(const void* ids, const void* weight, void* out, int se
                           int d_model, int vocab_size, int ids_dtype, int dtype,
                           hipStream_t stream);
 
+/* --------------------------------------------------------------------------
+ * Llama attention plumbing (extensions; no single reference op).
+ *
+ * teeny_qkv_rope_split: the fused QKV projection output qkv
+ *   [B, seq_len, (Hq + 2*Hkv) * D] -> q_out [B, Hq, seq_len, D] with RoPE,
+ *   and K (with RoPE) / V written into caches [B, Hkv, cache_len, D] at rows
+ *   pos0 .. pos0+seq_len-1; RoPE positions are absolute (pos0 + s).  Fuses
+ *   the reference's TransposeHeadsOp x3 + RopeOp x2 (src/layers/attention.rs:97-123)
+ *   with their arithmetic (transpose_heads.rs:65-67, rope.rs:86-96).
+ * teeny_decode_attention: one query row per (b, q head), q [B, Hq, D],
+ *   against cache rows 0 .. n_keys-1 (all visible: the newest query is the
+ *   last position), o [B, Hq, D].  Split-K over 256-key chunks; workspace
+ *   teeny_decode_attention_workspace_bytes(...).  The reference recomputes
+ *   the prefix instead (examples/llama_generate.rs:373-381).
+ *   head_dim: a power of two from 8 to 128; Hq / Hkv <= 16.
+ * ------------------------------------------------------------------------ */
+int teeny_qkv_rope_split(const void* qkv, void* q_out, void* k_cache, void* v_cache, int batch,
+                         int seq_len, int pos0, int cache_len, int n_heads_q, int n_heads_kv,
+                         int head_dim, float ln_rope_base, int dtype, hipStream_t stream);
+size_t teeny_decode_attention_workspace_bytes(int batch, int n_heads_q, int n_keys,
+                                              int head_dim);
+int teeny_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* o,
+                           int batch, int n_heads_q, int n_heads_kv, int n_keys, int cache_len,
+                           int head_dim, float softmax_scale, int dtype, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,7 +31,8 @@
   X(embed)               \
   X(fa2_f32)             \
   X(fa2_fwd_bf16)        \
-  X(fa2_bwd_bf16)
+  X(fa2_bwd_bf16)        \
+  X(llama)
 
 #define TEENY_CO_DECL(n) \
   extern "C" const unsigned char teeny_co_##n[]; \
@@ -577,6 +578,72 @@ int teeny_swiglu_fwd(const void* z, void* out, int M, int d_ff, int dtype, hipSt
 int teeny_swiglu_bwd(const void* grad, const void* z, void* dz, int M, int d_ff, int dtype,
                      hipStream_t stream) {
   return swiglu_impl(true, grad, z, dz, M, d_ff, dtype, stream);
+}
+
+int teeny_qkv_rope_split(const void* qkv, void* q_out, void* k_cache, void* v_cache, int batch,
+                         int seq_len, int pos0, int cache_len, int n_heads_q, int n_heads_kv,
+                         int head_dim, float ln_rope_base, int dtype, hipStream_t stream) {
+  if (!qkv || !q_out || !k_cache || !v_cache) return TEENY_ERR_NULL_POINTER;
+  if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
+  if (batch <= 0 || seq_len <= 0 || pos0 < 0 || n_heads_q <= 0 || n_heads_kv <= 0 ||
+      n_heads_q % n_heads_kv != 0 || head_dim <= 0 || cache_len < pos0 + seq_len ||
+      (long)batch * seq_len * (n_heads_q + 2 * n_heads_kv) * head_dim >= kMaxElems ||
+      (long)batch * n_heads_kv * cache_len * head_dim >= kMaxElems)
+    return TEENY_ERR_INVALID_SHAPE;
+  const int vn = dtype == TEENY_BF16 ? 8 : 4;
+  if (head_dim % vn != 0 || head_dim % 2 != 0) return TEENY_ERR_UNSUPPORTED;
+  if (!std::isfinite(ln_rope_base)) return TEENY_ERR_INVALID_VALUE;
+  const int htot = n_heads_q + 2 * n_heads_kv;
+  const long gy = (long)batch * ((htot + 15) / 16);
+  if (gy > 65535) return TEENY_ERR_INVALID_SHAPE;
+  char name[48];
+  snprintf(name, sizeof name, "teeny_qkv_rope_split_%s", dtype_tag(dtype));
+  void* args[] = {&qkv, &q_out, &k_cache, &v_cache, &seq_len, &pos0, &cache_len,
+                  &n_heads_q, &n_heads_kv, &head_dim, &ln_rope_base};
+  unsigned shmem = 16u * (unsigned)(head_dim / 2) * 8u;
+  return launch(name, dim3((seq_len + 15) / 16, (unsigned)gy), dim3(256), shmem, stream, args);
+}
+
+static int decode_chunks(int n_keys) { return (n_keys + 255) / 256; }
+
+size_t teeny_decode_attention_workspace_bytes(int batch, int n_heads_q, int n_keys,
+                                              int head_dim) {
+  if (batch <= 0 || n_heads_q <= 0 || n_keys <= 0 || head_dim <= 0) return 0;
+  size_t rows = (size_t)batch * n_heads_q * decode_chunks(n_keys);
+  return 2 * align256(rows * sizeof(float)) + align256(rows * head_dim * sizeof(float));
+}
+
+int teeny_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* o,
+                           int batch, int n_heads_q, int n_heads_kv, int n_keys, int cache_len,
+                           int head_dim, float softmax_scale, int dtype, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
+  if (!q || !k_cache || !v_cache || !o) return TEENY_ERR_NULL_POINTER;
+  if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
+  if (batch <= 0 || n_heads_q <= 0 || n_heads_kv <= 0 || n_heads_q % n_heads_kv != 0 ||
+      n_keys <= 0 || cache_len < n_keys || batch * n_heads_kv > 65535 ||
+      (long)batch * n_heads_kv * cache_len * head_dim >= kMaxElems)
+    return TEENY_ERR_INVALID_SHAPE;
+  if (n_heads_q / n_heads_kv > 16) return TEENY_ERR_UNSUPPORTED;
+  if (head_dim < 8 || head_dim > 128 || (head_dim & (head_dim - 1)) != 0)
+    return TEENY_ERR_UNSUPPORTED;
+  if (!std::isfinite(softmax_scale)) return TEENY_ERR_INVALID_VALUE;
+  if (!workspace ||
+      workspace_bytes < teeny_decode_attention_workspace_bytes(batch, n_heads_q, n_keys, head_dim))
+    return TEENY_ERR_WORKSPACE;
+  int n_chunks = decode_chunks(n_keys);
+  size_t rows = (size_t)batch * n_heads_q * n_chunks;
+  float* pm = (float*)workspace;
+  float* pl = (float*)((char*)workspace + align256(rows * sizeof(float)));
+  float* po = (float*)((char*)workspace + 2 * align256(rows * sizeof(float)));
+  char name[48];
+  snprintf(name, sizeof name, "teeny_decode_attn_partial_%s", dtype_tag(dtype));
+  void* a0[] = {&q, &k_cache, &v_cache, &pm, &pl, &po, &n_heads_q, &n_heads_kv,
+                &n_keys, &cache_len, &head_dim, &softmax_scale};
+  int rc = launch(name, dim3(n_chunks, batch * n_heads_kv), dim3(256), 0, stream, a0);
+  if (rc) return rc;
+  snprintf(name, sizeof name, "teeny_decode_attn_combine_%s", dtype_tag(dtype));
+  void* a1[] = {&pm, &pl, &po, &o, &n_chunks, &head_dim};
+  return launch(name, dim3(batch * n_heads_q), dim3(head_dim), 0, stream, a1);
 }
 
 int teeny_token_embed_fwd(const void* ids, const void* weight, void* out, int seq_len,

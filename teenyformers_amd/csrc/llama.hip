@@ -1,0 +1,254 @@
+// Llama attention plumbing around the flash-attention kernels.
+//
+// teeny_qkv_rope_split: the fused QKV projection output [B, S, (Hq+2Hkv)*D]
+//   -> Q [B, Hq, S, D] with RoPE, and K (RoPE) / V appended to a KV cache
+//   [B, Hkv, cache_len, D] at positions pos0 .. pos0+S-1.  One pass over HBM
+//   replaces the reference's three TransposeHeadsOp and two RopeOp launches
+//   (src/layers/attention.rs:97-123; transpose_heads.rs:49-71, rope.rs:57-97)
+//   with the same arithmetic: interleaved pairs, theta = fp32(pos) *
+//   fp32(exp_f64(fp32(k) * (-2 ln_base / D))), position = absolute position.
+//
+// teeny_decode_attn_*: one new query row per (b, q head) against the first
+//   n_keys cached keys (flash-decoding: split-K partials over 256-key chunks,
+//   then a log-sum-exp merge).  The reference has no KV cache and recomputes
+//   the whole prefix every step (examples/llama_generate.rs:373-381); this is
+//   the same attention row evaluated once.
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kPos = 16;    // positions per workgroup
+constexpr int kRows = 16;   // head rows (of Hq + 2 Hkv) per workgroup
+
+template <typename T>
+__device__ void qkv_rope_split(const T* __restrict__ qkv, T* __restrict__ q_out,
+                               T* __restrict__ k_cache, T* __restrict__ v_cache, int seq,
+                               int pos0, int cache_len, int hq, int hkv, int head_dim,
+                               float ln_base) {
+  extern __shared__ float2 cs_tab[];  // [kPos][head_dim / 2]
+  const int half = head_dim / 2;
+  const int s0 = blockIdx.x * kPos;
+  const int htot = hq + 2 * hkv;
+  const int rows_per_b = (htot + kRows - 1) / kRows;
+  const int b = blockIdx.y / rows_per_b;
+  const int h0 = (blockIdx.y - b * rows_per_b) * kRows;
+  const float c = (-2.0f * ln_base) / (float)head_dim;
+  for (int i = threadIdx.x; i < kPos * half; i += kThreads) {
+    int p = i / half, k = i - p * half;
+    float inv = (float)exp((double)((float)k * c));
+    float theta = (float)(pos0 + s0 + p) * inv;
+    float sn, cn;
+    sincosf(theta, &sn, &cn);
+    cs_tab[i] = make_float2(cn, sn);
+  }
+  __syncthreads();
+  constexpr int VN = Vec16<T>::N;
+  const int vpr = head_dim / VN;
+  const int total = kRows * kPos * vpr;
+  for (int i = threadIdx.x; i < total; i += kThreads) {
+    int v = i % vpr;
+    int r = i / vpr;
+    int p = r % kPos;
+    int hh = h0 + r / kPos;
+    int s = s0 + p;
+    if (s >= seq || hh >= htot) continue;
+    float in[VN];
+    Vec16<T>::load(qkv + ((long)b * seq + s) * htot * head_dim + (long)hh * head_dim + v * VN, in);
+    T* dst;
+    if (hh < hq)
+      dst = q_out + (((long)b * hq + hh) * seq + s) * head_dim;
+    else if (hh < hq + hkv)
+      dst = k_cache + (((long)b * hkv + (hh - hq)) * cache_len + pos0 + s) * head_dim;
+    else
+      dst = v_cache + (((long)b * hkv + (hh - hq - hkv)) * cache_len + pos0 + s) * head_dim;
+    float out[VN];
+    if (hh < hq + hkv) {
+      const float2* cs = cs_tab + p * half + v * (VN / 2);
+#pragma unroll
+      for (int j = 0; j < VN / 2; ++j) {
+        float x0 = in[2 * j], x1 = in[2 * j + 1];
+        out[2 * j] = x0 * cs[j].x - x1 * cs[j].y;
+        out[2 * j + 1] = x0 * cs[j].y + x1 * cs[j].x;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < VN; ++j) out[j] = in[j];
+    }
+    Vec16<T>::store(dst + v * VN, out);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention
+// ---------------------------------------------------------------------------
+constexpr int kChunk = 256;  // keys per split-K workgroup
+constexpr int kMaxGroup = 16;
+constexpr int kMaxD = 128;
+
+// grid (n_chunks, B * Hkv); q [B, Hq, D], caches [B, Hkv, cache_len, D].
+// Partials: m, l [B*Hq, n_chunks]; o [B*Hq, n_chunks, D] (unnormalised).
+template <typename T>
+__device__ void decode_partial(const T* __restrict__ q, const T* __restrict__ kc,
+                               const T* __restrict__ vc, float* __restrict__ pm,
+                               float* __restrict__ pl, float* __restrict__ po, int hq, int hkv,
+                               int n_keys, int cache_len, int head_dim, float scale) {
+  __shared__ float qs[kMaxGroup][kMaxD];
+  __shared__ float ps[kMaxGroup][kChunk];
+  __shared__ float red[kMaxGroup][kThreads / 64];
+  __shared__ float ohalf[kMaxGroup][kMaxD];
+  const int group = hq / hkv;
+  const int kvh = blockIdx.y;  // b * hkv + hk
+  const int b = kvh / hkv, hk = kvh - b * hkv;
+  const int chunk = blockIdx.x, n_chunks = gridDim.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const long qh0 = (long)b * hq + (long)hk * group;  // first q head of the group
+  for (int i = tid; i < group * head_dim; i += kThreads)
+    qs[i / head_dim][i % head_dim] = (float)q[(qh0 + i / head_dim) * head_dim + i % head_dim];
+  __syncthreads();
+
+  // scores: one key per thread
+  const int key = chunk * kChunk + tid;
+  const bool valid = key < n_keys;
+  float sc[kMaxGroup];
+#pragma unroll
+  for (int g = 0; g < kMaxGroup; ++g) sc[g] = 0.0f;
+  if (valid) {
+    const T* krow = kc + ((long)kvh * cache_len + key) * head_dim;
+    constexpr int VN = Vec16<T>::N;
+    for (int d0 = 0; d0 < head_dim; d0 += VN) {
+      float kv[VN];
+      Vec16<T>::load(krow + d0, kv);
+#pragma unroll
+      for (int g = 0; g < kMaxGroup; ++g) {
+        if (g >= group) break;
+#pragma unroll
+        for (int j = 0; j < VN; ++j) sc[g] += qs[g][d0 + j] * kv[j];
+      }
+    }
+  }
+  // per-head chunk max and sum
+  float mloc[kMaxGroup];
+#pragma unroll
+  for (int g = 0; g < kMaxGroup; ++g) {
+    if (g >= group) break;
+    float s = valid ? sc[g] * scale : -INFINITY;
+    sc[g] = s;
+    float m = wave_max(s);
+    if (lane == 0) red[g][wave] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < kMaxGroup; ++g) {
+    if (g >= group) break;
+    float m = red[g][0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red[g][w]);
+    mloc[g] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < kMaxGroup; ++g) {
+    if (g >= group) break;
+    float p = valid ? expf(sc[g] - mloc[g]) : 0.0f;
+    ps[g][tid] = p;
+    float l = wave_sum(p);
+    if (lane == 0) red[g][wave] = l;
+  }
+  __syncthreads();
+  // O[g][d] = sum_k p[g][k] V[k][d]: thread = (d, key half)
+  const int d = tid % head_dim;
+  const int part = tid / head_dim;             // which slice of the chunk's keys
+  const int nparts = kThreads / head_dim;      // 2 for D=128, 4 for D=64
+  const int kper = kChunk / nparts;
+  float acc[kMaxGroup];
+#pragma unroll
+  for (int g = 0; g < kMaxGroup; ++g) acc[g] = 0.0f;
+  if (part < nparts) {
+    const int kbeg = chunk * kChunk + part * kper;
+    const int kend = min(kbeg + kper, n_keys);
+    for (int kk = kbeg; kk < kend; ++kk) {
+      float vv = (float)vc[((long)kvh * cache_len + kk) * head_dim + d];
+      const int j = kk - chunk * kChunk;
+#pragma unroll
+      for (int g = 0; g < kMaxGroup; ++g) {
+        if (g >= group) break;
+        acc[g] += ps[g][j] * vv;
+      }
+    }
+  }
+  // reduce the key slices through LDS (slices 1.. add into slice 0)
+  for (int sl = 1; sl < nparts; ++sl) {
+    if (part == sl) {
+#pragma unroll
+      for (int g = 0; g < kMaxGroup; ++g) {
+        if (g >= group) break;
+        ohalf[g][d] = acc[g];
+      }
+    }
+    __syncthreads();
+    if (part == 0) {
+#pragma unroll
+      for (int g = 0; g < kMaxGroup; ++g) {
+        if (g >= group) break;
+        acc[g] += ohalf[g][d];
+      }
+    }
+    __syncthreads();
+  }
+  if (part == 0) {
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+      if (g >= group) break;
+      const long row = (qh0 + g) * n_chunks + chunk;
+      po[row * head_dim + d] = acc[g];
+      if (d == 0) {
+        float l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; ++w) l += red[g][w];
+        pm[row] = mloc[g];
+        pl[row] = l;
+      }
+    }
+  }
+}
+
+// grid B*Hq, block head_dim threads: merge the chunk partials.
+template <typename T>
+__device__ void decode_combine(const float* __restrict__ pm, const float* __restrict__ pl,
+                               const float* __restrict__ po, T* __restrict__ o, int n_chunks,
+                               int head_dim) {
+  const long row = blockIdx.x;
+  const int d = threadIdx.x;
+  float m = -INFINITY;
+  for (int c = 0; c < n_chunks; ++c) m = fmaxf(m, pm[row * n_chunks + c]);
+  float l = 0.0f, acc = 0.0f;
+  for (int c = 0; c < n_chunks; ++c) {
+    float w = expf(pm[row * n_chunks + c] - m);
+    l += pl[row * n_chunks + c] * w;
+    acc += po[(row * n_chunks + c) * head_dim + d] * w;
+  }
+  o[row * head_dim + d] = (T)(acc / l);
+}
+
+}  // namespace
+
+#define TEENY_LLAMA_INST(TN, T)                                                                 \
+  extern "C" __global__ __launch_bounds__(256) void teeny_qkv_rope_split_##TN(                 \
+      const T* qkv, T* q_out, T* k_cache, T* v_cache, int seq, int pos0, int cache_len, int hq, \
+      int hkv, int head_dim, float ln_base) {                                                   \
+    qkv_rope_split<T>(qkv, q_out, k_cache, v_cache, seq, pos0, cache_len, hq, hkv, head_dim,    \
+                      ln_base);                                                                 \
+  }                                                                                             \
+  extern "C" __global__ __launch_bounds__(256) void teeny_decode_attn_partial_##TN(            \
+      const T* q, const T* kc, const T* vc, float* pm, float* pl, float* po, int hq, int hkv,   \
+      int n_keys, int cache_len, int head_dim, float scale) {                                   \
+    decode_partial<T>(q, kc, vc, pm, pl, po, hq, hkv, n_keys, cache_len, head_dim, scale);      \
+  }                                                                                             \
+  extern "C" __global__ __launch_bounds__(256) void teeny_decode_attn_combine_##TN(            \
+      const float* pm, const float* pl, const float* po, T* o, int n_chunks, int head_dim) {    \
+    decode_combine<T>(pm, pl, po, o, n_chunks, head_dim);                                       \
+  }
+
+TEENY_LLAMA_INST(f32, float)
+TEENY_LLAMA_INST(bf16, bf16)

@@ -1,0 +1,248 @@
+"""Llama decoder model over the HIP ops: the reference's layers with batch,
+GQA, a KV cache and bf16 weights.
+
+Mirrors (reference file:line):
+  LlamaConfig                     src/config.rs:62-179 (n_kv_heads honoured, unlike
+                                  Llama::new at src/llama.rs:53)
+  MultiHeadAttention.forward      src/layers/attention.rs:83-148: projections ->
+                                  transpose_heads -> RoPE -> causal FA2 -> merge_heads -> o_proj
+  FeedForward.forward             src/layers/ffn.rs:47-56: fused gate||up -> SwiGLU -> down
+  LlamaBlock.forward              src/layers/llama_block.rs:55-65: x + attn(rms(x)), then
+                                  + ffn(rms(.))
+  Llama.forward                   src/llama.rs:65-81: embed -> blocks -> norm -> tied lm_head
+  generate_recompute              examples/llama_generate.rs:373-391: greedy decoding by
+                                  recomputing the whole sequence each step
+
+MI355X-specific structure (same arithmetic):
+  * q/k/v projections are one GEMM against the concatenated weight, and
+    teeny_qkv_rope_split does the three head transposes, both RoPEs and the
+    KV-cache write in one pass;
+  * every residual add is fused into the next RMSNorm (teeny_fused_add_rmsnorm);
+  * prefill runs the causal FA2 kernel over the cache; each decode step runs
+    teeny_decode_attention over the cached keys;
+  * Linear layers (teeny-core's external `Linear`, src/layers/mod.rs:54-58,
+    y = x W^T with W [out, in]) are hipBLASLt GEMMs through torch.
+"""
+from __future__ import annotations
+
+import dataclasses
+import json
+import math
+
+import torch
+import torch.nn.functional as F
+
+from . import ops
+
+
+@dataclasses.dataclass
+class LlamaConfig:
+    """src/config.rs:62-82; defaults from src/config.rs:165-179."""
+    d_model: int = 4096
+    n_heads: int = 32
+    n_layers: int = 32
+    vocab_size: int = 32000
+    max_seq_len: int = 4096
+    eps: float = 1e-5
+    rope_base: float = 10000.0
+    intermediate_size: int | None = None
+    n_kv_heads_: int | None = None
+
+    def head_dim(self) -> int:  # config.rs:138-140
+        return self.d_model // self.n_heads
+
+    def d_ff(self) -> int:  # config.rs:146-153: intermediate_size or ceil(8d/3 / 64) * 64
+        if self.intermediate_size is not None:
+            return self.intermediate_size
+        raw = -(-8 * self.d_model // 3)
+        return -(-raw // 64) * 64
+
+    def softmax_scale(self) -> float:  # config.rs:156-158 (f32)
+        return float(torch.tensor(1.0, dtype=torch.float32)
+                     / torch.tensor(float(self.head_dim()), dtype=torch.float32).sqrt())
+
+    def n_kv_heads(self) -> int:  # config.rs:161-163
+        return self.n_kv_heads_ if self.n_kv_heads_ is not None else self.n_heads
+
+    @classmethod
+    def from_hf_json(cls, path: str) -> "LlamaConfig":
+        """HF config.json subset (config.rs:84-134)."""
+        with open(path) as f:
+            hf = json.load(f)
+        return cls(d_model=hf["hidden_size"], n_heads=hf["num_attention_heads"],
+                   n_layers=hf["num_hidden_layers"], vocab_size=hf["vocab_size"],
+                   max_seq_len=hf.get("max_position_embeddings", 4096),
+                   eps=hf.get("rms_norm_eps", 1e-5), rope_base=hf.get("rope_theta", 10000.0),
+                   intermediate_size=hf.get("intermediate_size"),
+                   n_kv_heads_=hf.get("num_key_value_heads"))
+
+
+def init_weights(cfg: LlamaConfig, dtype=torch.bfloat16, device="cuda", std: float = 0.02,
+                 seed: int = 0) -> dict:
+    """Random weights ~ N(0, std) (norm weights 1), HF names
+    (src/llama.rs:66-80, src/layers/*.rs name scopes); q|k|v and gate|up are
+    stored concatenated along rows, gate first (src/loader.rs:49-55)."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    D, Hq, Hkv, F_ = cfg.head_dim(), cfg.n_heads, cfg.n_kv_heads(), cfg.d_ff()
+    d = cfg.d_model
+
+    def rnd(*shape):
+        return (torch.randn(shape, generator=gen, device=device, dtype=torch.float32) * std).to(dtype)
+
+    w = {"model.embed_tokens.weight": rnd(cfg.vocab_size, d),
+         "model.norm.weight": torch.ones(d, dtype=dtype, device=device)}
+    for i in range(cfg.n_layers):
+        p = f"model.layers.{i}."
+        w[p + "input_layernorm.weight"] = torch.ones(d, dtype=dtype, device=device)
+        w[p + "post_attention_layernorm.weight"] = torch.ones(d, dtype=dtype, device=device)
+        w[p + "self_attn.qkv_proj.weight"] = rnd((Hq + 2 * Hkv) * D, d)
+        w[p + "self_attn.o_proj.weight"] = rnd(d, Hq * D)
+        w[p + "mlp.gate_up_proj.weight"] = rnd(2 * F_, d)
+        w[p + "mlp.down_proj.weight"] = rnd(d, F_)
+    return w
+
+
+class KVCache:
+    """Per-layer K/V caches [B, Hkv, capacity, D], zero-initialised (rows past
+    the written prefix are masked by causality and must hold finite values)."""
+
+    def __init__(self, cfg: LlamaConfig, batch: int, capacity: int, dtype, device="cuda"):
+        shape = (batch, cfg.n_kv_heads(), capacity, cfg.head_dim())
+        self.k = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(cfg.n_layers)]
+        self.v = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(cfg.n_layers)]
+        self.capacity = capacity
+        self.length = 0
+
+
+class Llama:
+    """Forward passes of the Llama model (src/llama.rs:40-82) on the HIP ops."""
+
+    def __init__(self, cfg: LlamaConfig, weights: dict):
+        self.cfg = cfg
+        self.w = weights
+        self.decode_ws = None
+
+    # -- one block (src/layers/llama_block.rs:55-65) -------------------------
+    def _attention(self, i: int, n1: torch.Tensor, cache: KVCache, pos0: int) -> torch.Tensor:
+        """src/layers/attention.rs:83-148 with GQA and a KV cache."""
+        cfg, w = self.cfg, self.w
+        B, S, d = n1.shape
+        Hq, Hkv, D = cfg.n_heads, cfg.n_kv_heads(), cfg.head_dim()
+        p = f"model.layers.{i}.self_attn."
+        qkv = F.linear(n1, w[p + "qkv_proj.weight"])  # [B, S, (Hq+2Hkv) D]
+        q = torch.empty((B, Hq, S, D), dtype=n1.dtype, device=n1.device)
+        ops.qkv_rope_split(qkv, q, cache.k[i], cache.v[i], pos0, Hq, Hkv, cfg.rope_base)
+        scale = cfg.softmax_scale()
+        if S == 1 and pos0 > 0:  # decode: the new row sees every cached key
+            if self.decode_ws is None:
+                self.decode_ws = torch.empty(
+                    ops._lib.lib().teeny_decode_attention_workspace_bytes(
+                        B, Hq, cache.capacity, D), dtype=torch.uint8, device=n1.device)
+            o = ops.decode_attention(q.view(B, Hq, D), cache.k[i], cache.v[i], pos0 + 1, scale,
+                                     workspace=self.decode_ws).view(B, Hq, 1, D)
+        else:
+            if pos0 != 0:
+                raise ValueError("prefill must start at position 0")
+            # causal FA2 over the cache: keys past S are masked (key > query)
+            o, _ = ops.flash_attn2_fwd(q, cache.k[i], cache.v[i], scale, causal=True)
+        return F.linear(ops.merge_heads(o), w[p + "o_proj.weight"])
+
+    def _ffn(self, i: int, n2: torch.Tensor) -> torch.Tensor:
+        """src/layers/ffn.rs:47-56."""
+        p = f"model.layers.{i}.mlp."
+        z = F.linear(n2, self.w[p + "gate_up_proj.weight"])
+        return F.linear(ops.swiglu(z), self.w[p + "down_proj.weight"])
+
+    def hidden(self, ids: torch.Tensor, cache: KVCache, pos0: int) -> torch.Tensor:
+        """Final-norm hidden states [B, S, d] for ids [B, S] at positions pos0..,
+        appending the new keys/values to `cache`."""
+        cfg, w = self.cfg, self.w
+        x = ops.token_embed(ids.to(torch.int32).contiguous(), w["model.embed_tokens.weight"])
+        eps = cfg.eps
+        delta = None
+        for i in range(cfg.n_layers):
+            p = f"model.layers.{i}."
+            if delta is None:
+                n1, _ = ops.rmsnorm(x, w[p + "input_layernorm.weight"], eps, want_rstd=False)
+            else:  # x = x + ffn(...) fused into this block's input norm
+                n1, x, _ = ops.fused_add_rmsnorm(delta, x, w[p + "input_layernorm.weight"], eps)
+            a = self._attention(i, n1, cache, pos0)
+            n2, x, _ = ops.fused_add_rmsnorm(a, x, w[p + "post_attention_layernorm.weight"], eps)
+            delta = self._ffn(i, n2)
+        y, _, _ = ops.fused_add_rmsnorm(delta, x, w["model.norm.weight"], eps)
+        cache.length = pos0 + ids.shape[1]
+        return y
+
+    def logits(self, h: torch.Tensor) -> torch.Tensor:
+        """Tied lm_head (src/layers/embedding.rs:159-167): h @ E^T."""
+        return F.linear(h, self.w["model.embed_tokens.weight"])
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        """All-position logits [B, S, vocab] (src/llama.rs:65-81)."""
+        B, S = ids.shape
+        cache = KVCache(self.cfg, B, S, self.w["model.norm.weight"].dtype, ids.device)
+        return self.logits(self.hidden(ids, cache, 0))
+
+    # -- generation -----------------------------------------------------------
+    def prefill(self, ids: torch.Tensor, capacity: int) -> tuple[KVCache, torch.Tensor]:
+        """Prompt pass: returns the cache and the last position's logits."""
+        B, S = ids.shape
+        cache = KVCache(self.cfg, B, capacity, self.w["model.norm.weight"].dtype, ids.device)
+        h = self.hidden(ids, cache, 0)
+        return cache, self.logits(h[:, -1])
+
+    def decode_step(self, cache: KVCache, ids: torch.Tensor) -> torch.Tensor:
+        """One token per sequence (ids [B, 1]) -> next-token logits [B, vocab]."""
+        h = self.hidden(ids, cache, cache.length)
+        return self.logits(h[:, -1])
+
+    def generate(self, prompt: torch.Tensor, n_new: int) -> torch.Tensor:
+        """Greedy decoding with the KV cache -> generated ids [B, n_new]."""
+        cache, logits = self.prefill(prompt, prompt.shape[1] + n_new)
+        out = []
+        for _ in range(n_new):
+            nxt = torch.argmax(logits, dim=-1, keepdim=True)  # greedy (llama_generate.rs:252-257)
+            out.append(nxt)
+            if len(out) == n_new:
+                break
+            logits = self.decode_step(cache, nxt)
+        return torch.cat(out, dim=1)
+
+    def generate_recompute(self, prompt: torch.Tensor, n_new: int) -> torch.Tensor:
+        """The reference's method (examples/llama_generate.rs:373-391): every
+        step recomputes the whole sequence and takes the last row's argmax."""
+        seq = prompt
+        out = []
+        for _ in range(n_new):
+            B, S = seq.shape
+            cache = KVCache(self.cfg, B, S, self.w["model.norm.weight"].dtype, seq.device)
+            h = self.hidden(seq, cache, 0)
+            nxt = torch.argmax(self.logits(h[:, -1]), dim=-1, keepdim=True)
+            out.append(nxt)
+            seq = torch.cat([seq, nxt], dim=1)
+        return torch.cat(out, dim=1)
+
+
+def block_forward(cfg: LlamaConfig, w: dict, x: torch.Tensor, layer: int = 0) -> torch.Tensor:
+    """One LlamaBlock forward, x [B, S, d] -> [B, S, d] (src/layers/llama_block.rs:55-65)."""
+    model = Llama(cfg, w)
+    B, S, d = x.shape
+    cache = KVCache(dataclasses.replace(cfg, n_layers=layer + 1), B, S, x.dtype, x.device)
+    p = f"model.layers.{layer}."
+    n1, _ = ops.rmsnorm(x, w[p + "input_layernorm.weight"], cfg.eps, want_rstd=False)
+    a = model._attention(layer, n1, cache, 0)
+    n2, x2, _ = ops.fused_add_rmsnorm(a, x, w[p + "post_attention_layernorm.weight"], cfg.eps)
+    f = model._ffn(layer, n2)
+    return x2 + f
+
+
+def prefill_flops(cfg: LlamaConfig, batch: int, seq: int, last_logits_only: bool = True) -> float:
+    """Matrix FLOPs of a prefill: 2 * params * tokens for the layers, causal
+    attention 4 * S^2/2 * Hq * D per layer and sequence, and the lm_head."""
+    d, D, Hq, Hkv, F_ = cfg.d_model, cfg.head_dim(), cfg.n_heads, cfg.n_kv_heads(), cfg.d_ff()
+    per_layer = d * (Hq + 2 * Hkv) * D + Hq * D * d + d * 2 * F_ + F_ * d
+    tokens = batch * seq
+    f = 2.0 * per_layer * tokens * cfg.n_layers
+    f += cfg.n_layers * batch * 4.0 * seq * seq / 2 * Hq * D
+    f += 2.0 * d * cfg.vocab_size * (batch if last_logits_only else tokens)
+    return f

@@ -324,3 +324,38 @@ def token_embed(ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     call("teeny_token_embed_fwd", _p(ids), _p(weight), _p(out), ids.numel(), Dm, V, idc,
          _code(weight), _stream())
     return out
+
+
+# ---------------------------------------------------------------------------
+# Llama attention plumbing
+# ---------------------------------------------------------------------------
+
+def _ln(rope_base: float) -> float:
+    return float(torch.tensor(rope_base, dtype=torch.float32).log().item())
+
+
+def qkv_rope_split(qkv, q_out, k_cache, v_cache, pos0: int, n_heads_q: int, n_heads_kv: int,
+                   rope_base: float):
+    """qkv [B, S, (Hq+2Hkv)*D] -> q_out [B, Hq, S, D] (RoPE) and K (RoPE) / V
+    written to caches [B, Hkv, L, D] at rows pos0 .. pos0+S-1."""
+    _dev(qkv, q_out, k_cache, v_cache)
+    B, S, _ = qkv.shape
+    D = q_out.shape[-1]
+    call("teeny_qkv_rope_split", _p(qkv), _p(q_out), _p(k_cache), _p(v_cache), B, S, pos0,
+         k_cache.shape[2], n_heads_q, n_heads_kv, D, _ln(rope_base), _code(qkv), _stream())
+
+
+def decode_attention(q, k_cache, v_cache, n_keys: int, softmax_scale: float | None = None,
+                     out=None, workspace=None):
+    """q [B, Hq, D] (one new row per head) over cache rows 0 .. n_keys-1."""
+    _dev(q, k_cache, v_cache)
+    B, Hq, D = q.shape
+    Hkv, L = k_cache.shape[1], k_cache.shape[2]
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    need = _lib.lib().teeny_decode_attention_workspace_bytes(B, Hq, n_keys, D)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    out = torch.empty_like(q) if out is None else out
+    call("teeny_decode_attention", _p(q), _p(k_cache), _p(v_cache), _p(out), B, Hq, Hkv,
+         n_keys, L, D, scale, _code(q), _p(workspace), workspace.numel(), _stream())
+    return out
