@@ -12,9 +12,16 @@ are resident in HBM before timing.  Prints one JSON line:
   cpu_baseline the oracle's restatement of the reference kernels (fp32,
               every key of every row, as the reference loops) timed on a
               sample of heads on this host's cores
-  detail      per-op numbers (forward, backward, each kernel)
+  detail      per-op numbers (forward, backward, each kernel), plus the other
+              configurations: long-context GQA FA2 (B1 Hq64 Hkv8 D128,
+              S=16384 and the ragged 8191, 1% of K rows x8), one Llama block
+              forward (B4 S2048 d2048, Hq32/Hkv8, F8192, bf16), and the
+              Llama-3-8B-shaped model (32 layers, d4096, Hq32/Hkv8, F14336,
+              vocab 128256, random N(0, 0.02) bf16 weights): prefill of 16 x 512
+              tokens and 128 greedy KV-cached decode steps
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                       [--no-extra]
 """
 from __future__ import annotations
 
@@ -47,6 +54,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=48,
                     help="heads of the workload the CPU baseline times")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the long-context GQA, Llama block and Llama-8B measurements")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed steps, run one head transpose (a pure copy) of "
                          "Q's 256 MiB, the known-size reference for HBM byte counters")
@@ -154,10 +163,113 @@ def main() -> int:
         },
     }
 
+    if not args.no_extra:
+        del q, k, v, do, o, lse, dq, dk, dv, ws
+        torch.cuda.empty_cache()
+        out["detail"]["fa2_gqa_long"] = bench_gqa_long(torch, ops)
+        out["detail"]["llama_block"] = bench_llama_block(torch)
+        out["detail"]["llama_8b_shape"] = bench_llama_8b(torch)
+        torch.cuda.empty_cache()
+        gen = torch.Generator(device=dev).manual_seed(1234)
+        q, k, v, do = (torch.randn(shape, generator=gen, device=dev).to(torch.bfloat16)
+                       for _ in range(4))
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(q, k, v, do, scale, args.cpu_heads)
     print(json.dumps(out), flush=True)
     return 0
+
+
+def _time(torch, fn, reps: int, warmup: int = 1) -> float:
+    """Mean milliseconds of fn() over reps calls (device-synchronised)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / reps
+
+
+def bench_gqa_long(torch, ops):
+    """Causal GQA FA2 fwd+bwd, B1 Hq64 Hkv8 D128, S = 16384 and 8191, 1% of K
+    rows scaled x8."""
+    res = {}
+    for S_ in (16384, 8191):
+        gen = torch.Generator(device="cuda").manual_seed(S_)
+        q = torch.randn((1, 64, S_, 128), generator=gen, device="cuda").to(torch.bfloat16)
+        k = torch.randn((1, 8, S_, 128), generator=gen, device="cuda")
+        idx = torch.randperm(S_, generator=gen, device="cuda")[: max(1, S_ // 100)]
+        k[:, :, idx] *= 8
+        k = k.to(torch.bfloat16)
+        v = torch.randn((1, 8, S_, 128), generator=gen, device="cuda").to(torch.bfloat16)
+        do = torch.randn_like(q)
+        sc = 1.0 / math.sqrt(128)
+        o, lse = ops.flash_attn2_fwd(q, k, v, sc, True)
+        fwd_ms = _time(torch, lambda: ops.flash_attn2_fwd(q, k, v, sc, True, out=o, lse=lse), 5)
+        bwd_ms = _time(torch, lambda: ops.flash_attn2_bwd(q, k, v, o, lse, do, sc, True), 5)
+        f = fwd_flops(1, 64, S_, S_, 128)
+        res[f"S{S_}"] = {"fwd_ms": round(fwd_ms, 3), "bwd_ms": round(bwd_ms, 3),
+                         "fwd_tflops": round(f / fwd_ms / 1e9, 1),
+                         "bwd_tflops": round(2.5 * f / bwd_ms / 1e9, 1),
+                         "fwd_pct_peak": round(f / fwd_ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+                         "bwd_pct_peak": round(2.5 * f / bwd_ms / 1e9 / PEAK_BF16_TFLOPS, 4)}
+        del q, k, v, do, o, lse
+    return res
+
+
+def bench_llama_block(torch):
+    """One Llama block forward, B4 S2048 d2048, Hq32 Hkv8 D64, F8192, bf16."""
+    from teenyformers_amd import llama
+
+    cfg = llama.LlamaConfig(d_model=2048, n_heads=32, n_layers=1, vocab_size=32, eps=1e-5,
+                            rope_base=5e5, intermediate_size=8192, n_kv_heads_=8)
+    w = llama.init_weights(cfg, dtype=torch.bfloat16, seed=11)
+    x = torch.randn((4, 2048, 2048), device="cuda").to(torch.bfloat16)
+    ms = _time(torch, lambda: llama.block_forward(cfg, w, x), 10)
+    f = llama.prefill_flops(cfg, 4, 2048) - 2.0 * 2048 * 32 * 4  # no lm_head
+    return {"ms": round(ms, 3), "tflops": round(f / ms / 1e9, 1),
+            "pct_peak": round(f / ms / 1e9 / PEAK_BF16_TFLOPS, 4), "flop": f}
+
+
+def bench_llama_8b(torch):
+    """Llama-3-8B-shaped model: prefill 16 x 512 tokens, then 128 greedy
+    KV-cached decode steps (random N(0, 0.02) bf16 weights, uniform ids)."""
+    from teenyformers_amd import llama
+
+    cfg = llama.LlamaConfig(d_model=4096, n_heads=32, n_layers=32, vocab_size=128256,
+                            eps=1e-5, rope_base=5e5, intermediate_size=14336, n_kv_heads_=8)
+    w = llama.init_weights(cfg, dtype=torch.bfloat16, seed=12)
+    model = llama.Llama(cfg, w)
+    Bq, Sp, n_new = 16, 512, 128
+    ids = torch.randint(0, cfg.vocab_size, (Bq, Sp), device="cuda")
+    cache_holder = {}
+
+    def prefill():
+        cache_holder["c"], cache_holder["l"] = model.prefill(ids, Sp + n_new)
+
+    prefill_ms = _time(torch, prefill, 3)
+    cache, logits = cache_holder["c"], cache_holder["l"]
+    nxt = torch.argmax(logits, dim=-1, keepdim=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n_new):
+        logits = model.decode_step(cache, nxt)
+        nxt = torch.argmax(logits, dim=-1, keepdim=True)
+    torch.cuda.synchronize()
+    decode_ms = (time.perf_counter() - t0) * 1e3 / n_new
+    f = llama.prefill_flops(cfg, Bq, Sp)
+    wbytes = sum(t.numel() * t.element_size() for t in w.values())
+    del w, model, cache
+    return {"prefill_ms": round(prefill_ms, 2),
+            "prefill_tokens_per_s": round(Bq * Sp / prefill_ms * 1e3, 1),
+            "prefill_tflops": round(f / prefill_ms / 1e9, 1),
+            "prefill_pct_peak": round(f / prefill_ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+            "decode_ms_per_step": round(decode_ms, 3),
+            "decode_tokens_per_s": round(Bq / decode_ms * 1e3, 1),
+            "decode_weight_gbs": round(wbytes / decode_ms / 1e6, 1),
+            "decode_pct_hbm_peak": round(wbytes / decode_ms / 1e6 / PEAK_HBM_GBS, 4),
+            "batch": Bq, "prompt": Sp, "new_tokens": n_new}
 
 
 def traffic_from_profiles(kernel: str):
