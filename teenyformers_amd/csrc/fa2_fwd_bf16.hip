@@ -31,48 +31,60 @@ namespace {
 
 constexpr int BM = 128;  // query rows per workgroup
 constexpr int BN = 64;   // keys per iteration
-constexpr int KPAD = 8;   // K row padding: row stride = 4 mod 64 dwords (16-byte reads)
-constexpr int VPAD = 32;  // V row padding: row stride = 16 mod 64 dwords (transpose reads)
+constexpr int KBUF = 2;  // K tiles in flight: read by QK(i), loading i+1
+constexpr int VBUF = 3;  // V tiles: read by PV(i-1), waiting (i), loading (i+1)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescale = 8.0f;  // lazy-rescale threshold, log2 units
 
 DEVI float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
 DEVI bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-
 DEVI f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-template <int D>
-struct __attribute__((aligned(16))) FwdSmem {
-  bf16 k[2][BN][D + KPAD];
-  bf16 v[2][BN][D + VPAD];
-};
-
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 // ds_read_b64_tr_b16: within each 16-lane group, output lane i receives
 // element (i % 4) of the 8-byte chunks addressed by lanes i/4, i/4+4, i/4+8
-// and i/4+12 (measured on gfx950).  So if lane p of the group addresses row
-// r0 + p/4, columns c0 + 4*(p%4) .. +3 of a row-major tile, lane i receives
-// column c0 + i of rows r0 .. r0+3: a 4 x 16 block read transposed.
-DEVI u32x2 lds_read_tr(const bf16* p) {
+// and i/4+12 (measured on gfx950): lanes addressing a 4-row x 16-column block
+// of a row-major tile receive it transposed, one column per lane.
+DEVI u32x2 lds_read_tr(const char* p) {
   s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) s16x4*)(p));
   return __builtin_bit_cast(u32x2, r);
 }
+
+// Tiles are stored unpadded, 16-byte chunk L = row * (D/8) + column-chunk,
+// and XOR-swizzled within each 256-byte line (64 banks x 4 bytes):
+//   K (read by rows, 16 bytes per lane):   position ^= line % 16
+//   V (read by the 4-row transpose reads): position ^= 2 * (line % 4)
+// so 16 lanes of either read touch distinct bank groups, and both swizzles
+// repeat every 8 rows for D = 64 and D = 128 (the reads step by 8 rows).
+template <bool VLAYOUT>
+DEVI int swz_chunk(int L) {
+  const int line = L >> 4, pos = L & 15;
+  const int x = VLAYOUT ? ((line & 3) << 1) : (line & 15);
+  return (line << 4) | (pos ^ x);
+}
+
+template <int D>
+struct __attribute__((aligned(16))) FwdSmem {
+  char k[KBUF][BN * D * 2];
+  char v[VBUF][BN * D * 2];
+};
 
 template <int D, bool CAUSAL>
 __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict__ k,
                              const bf16* __restrict__ v, bf16* __restrict__ o,
                              float* __restrict__ lse, int nq, int nk, float scale, int hq, int hkv,
                              int num_m_blocks, int total_blocks) {
-  constexpr int DC = D / 16;              // d-chunks of 16 for QK^T
-  constexpr int DT = D / 32;              // d-tiles of 32 for PV
-  constexpr int CPR = D / 8;              // 16-byte chunks per K row
-  constexpr int KCH = BN * CPR / 256;     // K (and V) chunks per thread
+  constexpr int DC = D / 16;           // d-chunks of 16 for QK^T
+  constexpr int DT = D / 32;           // d-tiles of 32 for PV
+  constexpr int CPR = D / 8;           // 16-byte chunks per row
+  constexpr int TCH = BN * CPR / 256;  // chunks per thread per tile (K and V each)
+  constexpr int TILE = BN * D * 2;     // bytes per tile
   __shared__ FwdSmem<D> sm;
 
   const int tid = threadIdx.x;
@@ -97,165 +109,179 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
     const bool ok = qrow < nq;
     const bf16* qp = q + ((long)bh * nq + (ok ? qrow : 0)) * D + 8 * g;
 #pragma unroll
-    for (int c = 0; c < DC; ++c) {
-      u32x4 t = ok ? *reinterpret_cast<const u32x4*>(qp + 16 * c) : u32x4{0, 0, 0, 0};
-      qreg[c] = as_bf16x8(t);
-    }
+    for (int c = 0; c < DC; ++c)
+      qreg[c] = as_bf16x8(ok ? *reinterpret_cast<const u32x4*>(qp + 16 * c) : u32x4{0, 0, 0, 0});
   }
 
   int kend = nk;
   if (CAUSAL) kend = min(nk, m0 + BM);
   const int n_iter = (kend + BN - 1) / BN;
 
-  // ---- global -> register staging of one K/V tile (row-major 16-byte chunks)
-  u32x4 kstage[KCH], vstage[KCH];
-  auto load_tile = [&](int kbase) {
-    if (kbase + BN <= nk) {  // interior tile: no bounds checks
+  // ---- direct global -> LDS tile loads --------------------------------------
+  // Load i of a wave writes LDS chunks (i*256 + wave*64 + lane) of the tile;
+  // each lane fetches the tile chunk that the swizzle puts there.
+  int k_src[TCH], v_src[TCH];  // element offsets of those chunks within a tile
 #pragma unroll
-      for (int i = 0; i < KCH; ++i) {
-        int c = i * 256 + tid;
-        long off = (long)(kbase + c / CPR) * D + (c % CPR) * 8;
-        kstage[i] = *reinterpret_cast<const u32x4*>(kb + off);
-        vstage[i] = *reinterpret_cast<const u32x4*>(vb + off);
-      }
-    } else {
+  for (int i = 0; i < TCH; ++i) {
+    const int P = i * 256 + wave * 64 + lane;
+    const int Lk = swz_chunk<false>(P), Lv = swz_chunk<true>(P);  // (an involution)
+    k_src[i] = (Lk / CPR) * D + (Lk % CPR) * 8;
+    v_src[i] = (Lv / CPR) * D + (Lv % CPR) * 8;
+  }
+  auto load_tile = [&](int it) {
+    const int kbase = it * BN;
+    char* kdst = sm.k[it % KBUF] + wave * 64 * 16;
+    char* vdst = sm.v[it % VBUF] + wave * 64 * 16;
+    const bf16* kt = kb + (long)kbase * D;
+    const bf16* vt = vb + (long)kbase * D;
+    const bool full = kbase + BN <= nk;
 #pragma unroll
-      for (int i = 0; i < KCH; ++i) {
-        int c = i * 256 + tid;
-        int key = kbase + c / CPR;
-        long off = (long)key * D + (c % CPR) * 8;
-        kstage[i] = key < nk ? *reinterpret_cast<const u32x4*>(kb + off) : u32x4{0, 0, 0, 0};
-        vstage[i] = key < nk ? *reinterpret_cast<const u32x4*>(vb + off) : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < TCH; ++i) {
+      int ko = k_src[i], vo = v_src[i];
+      if (!full) {  // rows past the sequence re-read its last row (masked later)
+        ko = min(ko / D, nk - 1 - kbase) * D + ko % D;
+        vo = min(vo / D, nk - 1 - kbase) * D + vo % D;
       }
+      __builtin_amdgcn_global_load_lds((const void*)(kt + ko), (lds_void*)(kdst + i * 4096), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vt + vo), (lds_void*)(vdst + i * 4096), 16, 0, 0);
     }
   };
-  auto store_tile = [&](int buf) {
+
+  // ---- LDS read offsets (bytes within a tile) -------------------------------
+  // K: lane reads row 32*kt + l32, column chunk 2c + g.
+  int k_off[DC];
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      int c = i * 256 + tid;
-      int row = c / CPR, col = (c % CPR) * 8;
-      *reinterpret_cast<u32x4*>(&sm.k[buf][row][col]) = kstage[i];
-      *reinterpret_cast<u32x4*>(&sm.v[buf][row][col]) = vstage[i];
-    }
-  };
-  // V^T operand addressing (lds_read_tr): lane p of 16-lane group G reads
-  // row 4*g + p/4 (+8 for the second half), columns 16*(G%2) + 4*(p%4), so
-  // lane (l32, g) receives V[key][32t + l32] for the keys 16hh + 4g + 0..3
-  // and 16hh + 8 + 4g + 0..3: the order the P^T accumulator holds them in.
-  const int tr_row = 4 * g + ((lane & 15) >> 2);
-  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  for (int c = 0; c < DC; ++c) k_off[c] = swz_chunk<false>(l32 * CPR + 2 * c + g) * 16;
+  // V^T: lane p of 16-lane group G reads row 4g + p/4 (+8, +16hh, +32kt) and
+  // 8 bytes at column 32t + 16(G%2) + 4(p%4); rows differing by 8 share the
+  // swizzle, so only the column tile t needs its own offset.
+  const int vr = 4 * g + ((lane & 15) >> 2);
+  int v_off[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    const int col = 32 * t + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    v_off[t] = swz_chunk<true>(vr * CPR + col / 8) * 16 + (col % 8) * 2;
+  }
+  constexpr int ROW8 = 8 * D * 2;  // bytes of 8 rows (a swizzle-invariant step)
 
   // ---- running state ---------------------------------------------------------
   f32x16 acc_o[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc_o[t] = f32x16{};
-  // m_run: the reference max of this lane's query row in log2 units.  It is
-  // raised lazily: only when some row of the wave sees a max more than
-  // kRescale above its m_run are O and l rescaled, so p = 2^(t - m_run) stays
+  // m_run is raised lazily: only when some row of the wave sees a max more
+  // than kRescale above it are O and l rescaled, so p = 2^(t - m_run) stays
   // below 2^kRescale (exact in fp32 and representable in bf16).
   float m_run = -INFINITY;
   float l_run = 0.0f;  // this lane's partial row sum (its 16 of every 32 keys)
   const float sl2 = scale * kLog2e;
 
-  if (n_iter > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
+  // P of the previous tile (B operand of its delayed PV) and its activity
+  uint32_t pprev[2][8];
+  bool prev_act0 = false, prev_act1 = false;
+  int prev_buf = 0;
+
+  auto pv = [&](int vbuf, bool a1) {
+    const char* vt = sm.v[vbuf];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      if (kt == 1 && !a1) break;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        bf16x8 bop = as_bf16x8(u32x4{pprev[kt][4 * hh], pprev[kt][4 * hh + 1],
+                                     pprev[kt][4 * hh + 2], pprev[kt][4 * hh + 3]});
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          const char* p = vt + v_off[t] + (4 * kt + 2 * hh) * ROW8;
+          u32x2 a0 = lds_read_tr(p);
+          u32x2 a1v = lds_read_tr(p + ROW8);
+          acc_o[t] = mfma32(as_bf16x8(u32x4{a0[0], a0[1], a1v[0], a1v[1]}), bop, acc_o[t]);
+        }
+      }
+    }
+  };
+
+  if (n_iter > 0) load_tile(0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   for (int it = 0; it < n_iter; ++it) {
-    const int cur = it & 1;
     const int kbase = it * BN;
-    if (it + 1 < n_iter) load_tile(kbase + BN);
+    if (it + 1 < n_iter) load_tile(it + 1);
     // causal: a tile whose first key is past this wave's last row is all masked
     const bool act0 = !(CAUSAL && kbase > wave_qmax);
-    if (act0) {
+    const bool act1 = act0 && kbase + 32 < nk && !(CAUSAL && kbase + 32 > wave_qmax);
 
-    // ---- S^T = K Q^T for the two 32-key subtiles (chains interleaved) ----
-    const bool act1 = kbase + 32 < nk && !(CAUSAL && kbase + 32 > wave_qmax);
     f32x16 s0 = f32x16{}, s1 = f32x16{};
-    {
-      const bf16* k0 = &sm.k[cur][l32][8 * g];
-      const bf16* k1 = &sm.k[cur][32 + l32][8 * g];
+    if (act0) {
+      // ---- S^T = K Q^T for the two 32-key subtiles (chains interleaved) ----
+      const char* kt0 = sm.k[it % KBUF];
 #pragma unroll
       for (int c = 0; c < DC; ++c) {
-        u32x4 a0 = *reinterpret_cast<const u32x4*>(k0 + 16 * c);
+        u32x4 a0 = *reinterpret_cast<const u32x4*>(kt0 + k_off[c]);
         s0 = mfma32(as_bf16x8(a0), qreg[c], s0);
         if (act1) {
-          u32x4 a1 = *reinterpret_cast<const u32x4*>(k1 + 16 * c);
+          u32x4 a1 = *reinterpret_cast<const u32x4*>(kt0 + 32 * D * 2 + k_off[c]);
           s1 = mfma32(as_bf16x8(a1), qreg[c], s1);
         }
       }
     }
+    // ---- the previous tile's O^T += V^T P^T runs while this tile's softmax
+    //      occupies the VALU ----
+    if (prev_act0) pv(prev_buf, prev_act1);
 
-    // ---- masking (boundary tiles only): raw scores -> -inf ----
-    const bool need_mask = (kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > m0 + wave * 32);
-    if (need_mask) {
+    if (act0) {
+      // ---- masking (boundary tiles only): raw scores -> -inf ----
+      const bool need_mask = (kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > m0 + wave * 32);
+      if (need_mask) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        int key = kbase + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (key >= nk || (CAUSAL && key > qrow)) s0[r] = -INFINITY;
-        key += 32;
-        if (!act1 || key >= nk || (CAUSAL && key > qrow)) s1[r] = -INFINITY;
-      }
-    } else if (!act1) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s1[r] = -INFINITY;
-    }
-
-    // ---- online softmax, log2 domain, lazy rescale ----
-    float mx = fmaxf(s0[0], s1[0]);
-#pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_tile = mx * sl2;  // scale > 0, so max(scale*s) = scale*max(s)
-    const bool grow = m_tile > m_run + kRescale;
-    if (__any(grow)) {
-      const float m_new = fmaxf(m_run, m_tile);
-      // 0 on a row's first tile; 1 for rows that did not grow (or saw no key)
-      const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int t = 0; t < DT; ++t) acc_o[t] *= alpha;
-    }
-    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-    float psum = 0.0f;
-    uint32_t pb[2][8];
-#pragma unroll
-    for (int r = 0; r < 16; r += 2) {
-      float p0 = fast_exp2(__builtin_fmaf(s0[r], sl2, -m_use));
-      float p1 = fast_exp2(__builtin_fmaf(s0[r + 1], sl2, -m_use));
-      float p2 = fast_exp2(__builtin_fmaf(s1[r], sl2, -m_use));
-      float p3 = fast_exp2(__builtin_fmaf(s1[r + 1], sl2, -m_use));
-      psum += (p0 + p1) + (p2 + p3);
-      pb[0][r >> 1] = pack_bf16x2(p0, p1);
-      pb[1][r >> 1] = pack_bf16x2(p2, p3);
-    }
-    l_run += psum;
-
-    // ---- O^T += V^T P^T ----
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      if (kt == 1 && !act1) break;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        bf16x8 bop = as_bf16x8(u32x4{pb[kt][4 * hh], pb[kt][4 * hh + 1], pb[kt][4 * hh + 2],
-                                     pb[kt][4 * hh + 3]});
-#pragma unroll
-        for (int t = 0; t < DT; ++t) {
-          const bf16* vp = &sm.v[cur][32 * kt + 16 * hh + tr_row][32 * t + tr_col];
-          u32x2 a0 = lds_read_tr(vp);
-          u32x2 a1 = lds_read_tr(vp + 8 * (D + VPAD));
-          acc_o[t] = mfma32(as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]}), bop, acc_o[t]);
+        for (int r = 0; r < 16; ++r) {
+          int key = kbase + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (key >= nk || (CAUSAL && key > qrow)) s0[r] = -INFINITY;
+          key += 32;
+          if (!act1 || key >= nk || (CAUSAL && key > qrow)) s1[r] = -INFINITY;
         }
+      } else if (!act1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s1[r] = -INFINITY;
       }
+      // ---- online softmax, log2 domain, lazy rescale ----
+      float mx = fmaxf(s0[0], s1[0]);
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_tile = mx * sl2;  // scale > 0, so max(scale*s) = scale*max(s)
+      const bool grow = m_tile > m_run + kRescale;
+      if (__any(grow)) {
+        const float m_new = fmaxf(m_run, m_tile);
+        // 0 on a row's first tile; 1 for rows that did not grow (or saw no key)
+        const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) acc_o[t] *= alpha;
+      }
+      const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+      float psum = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        float p0 = fast_exp2(__builtin_fmaf(s0[r], sl2, -m_use));
+        float p1 = fast_exp2(__builtin_fmaf(s0[r + 1], sl2, -m_use));
+        float p2 = fast_exp2(__builtin_fmaf(s1[r], sl2, -m_use));
+        float p3 = fast_exp2(__builtin_fmaf(s1[r + 1], sl2, -m_use));
+        psum += (p0 + p1) + (p2 + p3);
+        pprev[0][r >> 1] = pack_bf16x2(p0, p1);
+        pprev[1][r >> 1] = pack_bf16x2(p2, p3);
+      }
+      l_run += psum;
     }
-    }  // act0
+    prev_act0 = act0;
+    prev_act1 = act1;
+    prev_buf = it % VBUF;
 
-    if (it + 1 < n_iter) store_tile(cur ^ 1);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile it+1 have landed
     __syncthreads();
   }
+  if (prev_act0) pv(prev_buf, prev_act1);
 
   // ---- epilogue ----
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
