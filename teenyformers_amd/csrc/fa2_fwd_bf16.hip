@@ -38,13 +38,51 @@ constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescale = 8.0f;  // lazy-rescale threshold, log2 units
 
 DEVI float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// max of three floats in one instruction.  fmaxf on MFMA results costs an
+// extra canonicalising v_max per operand; scores are never signalling NaNs.
+DEVI float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// (value in lane l, value in lane l ^ 32) via v_permlane32_swap
+DEVI float other_half(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
+                                            __builtin_bit_cast(unsigned, x), false, false);
+  // lanes < 32 see (x[l], x[l+32]), lanes >= 32 see (x[l-32], x[l])
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+// acc + lo + hi of a packed bf16 pair (v_dot2c_f32_bf16 against (1, 1))
+DEVI float add_bf16x2(uint32_t w, float acc) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, w),
+                                         __builtin_bit_cast(b2, 0x3f803f80u), acc, false);
+}
 DEVI bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 DEVI f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// Instruction classes of __builtin_amdgcn_sched_group_barrier: the machine
+// scheduler fills the groups in the order they are declared.
+constexpr int kMfma = 0x008, kDsRead = 0x100;
+#define sched_group(mask, n) __builtin_amdgcn_sched_group_barrier((mask), (n), 0)
+// Keeps the computation of x above this point: values used only in the next
+// loop iteration would otherwise be sunk below the barrier that ends one,
+// out of the block they are scheduled in.
+template <typename T> DEVI void pin(T& x) { asm volatile("" : "+v"(x)); }
+
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
+
+// Raw buffer descriptor (stride 0, num_records in bytes) over [base, +bytes).
+DEVI __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+// 16 bytes per lane from buffer offset soff + voff into LDS at lds + 16 * lane
+DEVI void dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, soff, 0, 0);
+}
 
 // ds_read_b64_tr_b16: within each 16-lane group, output lane i receives
 // element (i % 4) of the 8-byte chunks addressed by lanes i/4, i/4+4, i/4+8
@@ -88,7 +126,8 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   __shared__ FwdSmem<D> sm;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  // wave-uniform (an SGPR): every branch on it is a scalar branch
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
 
   const int id = xcd_remap(blockIdx.x, total_blocks);
@@ -104,13 +143,12 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   const bf16* vb = v + kvh * (long)nk * D;
 
   // ---- Q rows -> registers (B operand) -------------------------------------
+  // rows past nq load row nq - 1: computed, never stored
   bf16x8 qreg[DC];
   {
-    const bool ok = qrow < nq;
-    const bf16* qp = q + ((long)bh * nq + (ok ? qrow : 0)) * D + 8 * g;
+    const bf16* qp = q + ((long)bh * nq + min(qrow, nq - 1)) * D + 8 * g;
 #pragma unroll
-    for (int c = 0; c < DC; ++c)
-      qreg[c] = as_bf16x8(ok ? *reinterpret_cast<const u32x4*>(qp + 16 * c) : u32x4{0, 0, 0, 0});
+    for (int c = 0; c < DC; ++c) qreg[c] = as_bf16x8(*reinterpret_cast<const u32x4*>(qp + 16 * c));
   }
 
   int kend = nk;
@@ -118,32 +156,36 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   const int n_iter = (kend + BN - 1) / BN;
 
   // ---- direct global -> LDS tile loads --------------------------------------
-  // Load i of a wave writes LDS chunks (i*256 + wave*64 + lane) of the tile;
-  // each lane fetches the tile chunk that the swizzle puts there.
-  int k_src[TCH], v_src[TCH];  // element offsets of those chunks within a tile
-#pragma unroll
-  for (int i = 0; i < TCH; ++i) {
-    const int P = i * 256 + wave * 64 + lane;
-    const int Lk = swz_chunk<false>(P), Lv = swz_chunk<true>(P);  // (an involution)
-    k_src[i] = (Lk / CPR) * D + (Lk % CPR) * 8;
-    v_src[i] = (Lv / CPR) * D + (Lv % CPR) * 8;
-  }
-  auto load_tile = [&](int it) {
+  // buffer_load ... lds (MUBUF, not FLAT: LDS waits elsewhere in the loop keep
+  // partial counts), address = SGPR descriptor of the head + SGPR tile offset
+  // + one VGPR per lane.  Load i of a wave writes LDS chunks
+  // (i*256 + wave*64 + lane) of the tile; each lane fetches the tile chunk
+  // that the swizzle puts there.  Adding 256 chunks (16 lines) leaves both
+  // swizzles unchanged, so a lane's chunks are one byte offset plus i * 4096.
+  const uint32_t k_src = swz_chunk<false>(wave * 64 + lane) * 16;
+  const uint32_t v_src = swz_chunk<true>(wave * 64 + lane) * 16;
+  const auto krsrc = make_rsrc(kb, nk * D * 2);
+  const auto vrsrc = make_rsrc(vb, nk * D * 2);
+  // it: tile index; koff / voff: byte offsets of its K and V buffers
+  auto load_tile = [&](int it, int koff, int voff) {
     const int kbase = it * BN;
-    char* kdst = sm.k[it % KBUF] + wave * 64 * 16;
-    char* vdst = sm.v[it % VBUF] + wave * 64 * 16;
-    const bf16* kt = kb + (long)kbase * D;
-    const bf16* vt = vb + (long)kbase * D;
-    const bool full = kbase + BN <= nk;
+    char* kdst = sm.k[0] + koff + wave * 64 * 16;
+    char* vdst = sm.v[0] + voff + wave * 64 * 16;
+    const int sbase = kbase * D * 2;
+    if (kbase + BN <= nk) {
 #pragma unroll
-    for (int i = 0; i < TCH; ++i) {
-      int ko = k_src[i], vo = v_src[i];
-      if (!full) {  // rows past the sequence re-read its last row (masked later)
-        ko = min(ko / D, nk - 1 - kbase) * D + ko % D;
-        vo = min(vo / D, nk - 1 - kbase) * D + vo % D;
+      for (int i = 0; i < TCH; ++i) {
+        dma16(krsrc, kdst + i * 4096, k_src, sbase + i * 4096);
+        dma16(vrsrc, vdst + i * 4096, v_src, sbase + i * 4096);
       }
-      __builtin_amdgcn_global_load_lds((const void*)(kt + ko), (lds_void*)(kdst + i * 4096), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(vt + vo), (lds_void*)(vdst + i * 4096), 16, 0, 0);
+    } else {  // rows past the sequence re-read its last row (masked later)
+      const int last = nk - 1 - kbase;
+#pragma unroll
+      for (int i = 0; i < TCH; ++i) {
+        const int ko = i * 4096 + k_src, vo = i * 4096 + v_src;
+        dma16(krsrc, kdst + i * 4096, min(ko / (2 * D), last) * (2 * D) + ko % (2 * D), sbase);
+        dma16(vrsrc, vdst + i * 4096, min(vo / (2 * D), last) * (2 * D) + vo % (2 * D), sbase);
+      }
     }
   };
 
@@ -172,119 +214,209 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   // than kRescale above it are O and l rescaled, so p = 2^(t - m_run) stays
   // below 2^kRescale (exact in fp32 and representable in bf16).
   float m_run = -INFINITY;
-  float l_run = 0.0f;  // this lane's partial row sum (its 16 of every 32 keys)
+  // this lane's partial row sums (its 16 of every 32 keys), two chains
+  float l_run = 0.0f, l_run2 = 0.0f;
   const float sl2 = scale * kLog2e;
 
-  // P of the previous tile (B operand of its delayed PV) and its activity
+  // P of the previous tile: the B operand of its delayed PV product
   uint32_t pprev[2][8];
-  bool prev_act0 = false, prev_act1 = false;
-  int prev_buf = 0;
+  uint32_t pnew[2][8];
 
-  auto pv = [&](int vbuf, bool a1) {
-    const char* vt = sm.v[vbuf];
+  // PV product j = (kt, hh, t): A = V^T rows t of keys 32kt + 16hh .. +16,
+  // two transpose reads; B = P of those keys
+  constexpr int NJ = 4 * DT;
+  constexpr int VPF = 2;  // V fragments are read this many products ahead
+  auto pv_read = [&](const char* vt, int j) {
+    const int t = j % DT, hh = (j / DT) & 1, kt = j / (2 * DT);
+    const char* p = vt + v_off[t] + (4 * kt + 2 * hh) * ROW8;
+    u32x2 a0 = lds_read_tr(p), a1 = lds_read_tr(p + ROW8);
+    return u32x4{a0[0], a0[1], a1[0], a1[1]};
+  };
+  auto pv_mfma = [&](int j, u32x4 a) {
+    const int t = j % DT, hh = (j / DT) & 1, kt = j / (2 * DT);
+    bf16x8 bop = as_bf16x8(u32x4{pprev[kt][4 * hh], pprev[kt][4 * hh + 1],
+                                 pprev[kt][4 * hh + 2], pprev[kt][4 * hh + 3]});
+    acc_o[t] = mfma32(as_bf16x8(a), bop, acc_o[t]);
+  };
+
+  // S^T = K Q^T for both 32-key subtiles of a tile (two interleaved chains,
+  // K fragments read KPF steps ahead)
+  auto qk = [&](const char* kt0, f32x16& s0, f32x16& s1) {
+    constexpr int KPF = 2;
+    s0 = f32x16{};
+    s1 = f32x16{};
+    u32x4 ra[DC], rb[DC];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      if (kt == 1 && !a1) break;
+    for (int c = 0; c < KPF; ++c) {
+      ra[c] = *reinterpret_cast<const u32x4*>(kt0 + k_off[c]);
+      rb[c] = *reinterpret_cast<const u32x4*>(kt0 + 32 * D * 2 + k_off[c]);
+    }
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        bf16x8 bop = as_bf16x8(u32x4{pprev[kt][4 * hh], pprev[kt][4 * hh + 1],
-                                     pprev[kt][4 * hh + 2], pprev[kt][4 * hh + 3]});
+    for (int c = 0; c < DC; ++c) {
+      if (c + KPF < DC) {
+        ra[c + KPF] = *reinterpret_cast<const u32x4*>(kt0 + k_off[c + KPF]);
+        rb[c + KPF] = *reinterpret_cast<const u32x4*>(kt0 + 32 * D * 2 + k_off[c + KPF]);
+      }
+      s0 = mfma32(as_bf16x8(ra[c]), qreg[c], s0);
+      s1 = mfma32(as_bf16x8(rb[c]), qreg[c], s1);
+    }
+    sched_group(kDsRead, 2 * KPF);
 #pragma unroll
-        for (int t = 0; t < DT; ++t) {
-          const char* p = vt + v_off[t] + (4 * kt + 2 * hh) * ROW8;
-          u32x2 a0 = lds_read_tr(p);
-          u32x2 a1v = lds_read_tr(p + ROW8);
-          acc_o[t] = mfma32(as_bf16x8(u32x4{a0[0], a0[1], a1v[0], a1v[1]}), bop, acc_o[t]);
-        }
+    for (int c = 0; c < DC; ++c) {
+      if (c + KPF < DC) sched_group(kDsRead, 2);
+      sched_group(kMfma, 2);
+    }
+  };
+
+  // raw scores of keys past the sequence or (causal) past the row -> -inf;
+  // only tiles that reach past nk or past the wave's first row need it
+  auto mask = [&](int kbase, f32x16& s0, f32x16& s1) {
+    if ((kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > m0 + wave * 32)) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        int key = kbase + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (key >= nk || (CAUSAL && key > qrow)) s0[r] = -INFINITY;
+        key += 32;
+        if (key >= nk || (CAUSAL && key > qrow)) s1[r] = -INFINITY;
       }
     }
   };
 
-  if (n_iter > 0) load_tile(0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  for (int it = 0; it < n_iter; ++it) {
-    const int kbase = it * BN;
-    if (it + 1 < n_iter) load_tile(it + 1);
-    // causal: a tile whose first key is past this wave's last row is all masked
-    const bool act0 = !(CAUSAL && kbase > wave_qmax);
-    const bool act1 = act0 && kbase + 32 < nk && !(CAUSAL && kbase + 32 > wave_qmax);
-
-    f32x16 s0 = f32x16{}, s1 = f32x16{};
-    if (act0) {
-      // ---- S^T = K Q^T for the two 32-key subtiles (chains interleaved) ----
-      const char* kt0 = sm.k[it % KBUF];
-#pragma unroll
-      for (int c = 0; c < DC; ++c) {
-        u32x4 a0 = *reinterpret_cast<const u32x4*>(kt0 + k_off[c]);
-        s0 = mfma32(as_bf16x8(a0), qreg[c], s0);
-        if (act1) {
-          u32x4 a1 = *reinterpret_cast<const u32x4*>(kt0 + 32 * D * 2 + k_off[c]);
-          s1 = mfma32(as_bf16x8(a1), qreg[c], s1);
-        }
-      }
+  // Row max of a tile in four pieces (so that they can sit between matrix
+  // products), the last one followed by the branch-free online-softmax
+  // update: grow = some row of the wave raised its maximum by more than
+  // kRescale (O must then be scaled by alpha before the next product), m_run
+  // and the row sums updated, m_use the exponent offset for this tile's P.
+  float mxa, mxb, alpha = 1.0f, m_use = 0.0f;
+  bool grow = false;
+  auto max_piece = [&](int u, const f32x16& s0, const f32x16& s1) {
+    if (u == 0) {
+      mxa = max3(s0[0], s0[1], s0[2]);
+      mxb = max3(s1[0], s1[1], s1[2]);
     }
-    // ---- the previous tile's O^T += V^T P^T runs while this tile's softmax
-    //      occupies the VALU ----
-    if (prev_act0) pv(prev_buf, prev_act1);
-
-    if (act0) {
-      // ---- masking (boundary tiles only): raw scores -> -inf ----
-      const bool need_mask = (kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > m0 + wave * 32);
-      if (need_mask) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          int key = kbase + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key >= nk || (CAUSAL && key > qrow)) s0[r] = -INFINITY;
-          key += 32;
-          if (!act1 || key >= nk || (CAUSAL && key > qrow)) s1[r] = -INFINITY;
-        }
-      } else if (!act1) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s1[r] = -INFINITY;
-      }
-      // ---- online softmax, log2 domain, lazy rescale ----
-      float mx = fmaxf(s0[0], s1[0]);
-#pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    for (int r = (u == 0 ? 3 : 4 * u + 1); r < 4 * u + 5 && r < 15; r += 2) {
+      mxa = max3(mxa, s0[r], s0[r + 1]);
+      mxb = max3(mxb, s1[r], s1[r + 1]);
+    }
+    if (u == 3) {
+      float mx = max3(mxa, mxb, max3(s0[15], s1[15], s1[15]));
+      mx = max3(mx, other_half(mx), mx);
       const float m_tile = mx * sl2;  // scale > 0, so max(scale*s) = scale*max(s)
-      const bool grow = m_tile > m_run + kRescale;
-      if (__any(grow)) {
-        const float m_new = fmaxf(m_run, m_tile);
-        // 0 on a row's first tile; 1 for rows that did not grow (or saw no key)
-        const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
-        m_run = m_new;
-        l_run *= alpha;
-#pragma unroll
-        for (int t = 0; t < DT; ++t) acc_o[t] *= alpha;
-      }
-      const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-      float psum = 0.0f;
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        float p0 = fast_exp2(__builtin_fmaf(s0[r], sl2, -m_use));
-        float p1 = fast_exp2(__builtin_fmaf(s0[r + 1], sl2, -m_use));
-        float p2 = fast_exp2(__builtin_fmaf(s1[r], sl2, -m_use));
-        float p3 = fast_exp2(__builtin_fmaf(s1[r + 1], sl2, -m_use));
-        psum += (p0 + p1) + (p2 + p3);
-        pprev[0][r >> 1] = pack_bf16x2(p0, p1);
-        pprev[1][r >> 1] = pack_bf16x2(p2, p3);
-      }
-      l_run += psum;
+      grow = __any(m_tile > m_run + kRescale);
+      const float m_new = grow ? fmaxf(m_run, m_tile) : m_run;
+      // 0 on a row's first tile; exactly 1 where the maximum is unchanged
+      alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+      l_run2 *= alpha;
+      m_use = m_run == -INFINITY ? 0.0f : m_run;
     }
-    prev_act0 = act0;
-    prev_act1 = act1;
-    prev_buf = it % VBUF;
+  };
+  // softmax of element pair q (0..15): half q%2 (s0 / s1), rows 2(q/2), +1
+  auto sm_pair = [&](const f32x16& s0, const f32x16& s1, float m_use, int q) {
+    const int hf = q & 1, r = (q >> 1) * 2;
+    const float x0 = hf ? s1[r] : s0[r], x1 = hf ? s1[r + 1] : s0[r + 1];
+    const uint32_t w = pack_bf16x2(fast_exp2(__builtin_fmaf(x0, sl2, -m_use)),
+                                   fast_exp2(__builtin_fmaf(x1, sl2, -m_use)));
+    pnew[hf][r >> 1] = w;
+    // the row sum adds the bf16 P that the PV product consumes
+    if (hf) l_run2 = add_bf16x2(w, l_run2);
+    else l_run = add_bf16x2(w, l_run);
+  };
+  // VALU work of one tile = 20 units: 4 row-max pieces, then 16 softmax pairs
+  auto run_unit = [&](int u, const f32x16& s0, const f32x16& s1) {
+    if (u < 4) max_piece(u, s0, s1);
+    else sm_pair(s0, s1, m_use, u - 4);
+  };
+  // the product after which unit u is issued (NJ = 16 or 8 products)
+  auto unit_slot = [](int u) {
+    if (NJ == 16) return u < 4 ? u : (u - 4 < 8 ? 4 + (u - 4) / 2 : u - 4);
+    return u < 4 ? u / 2 : (u - 4 < 12 ? 2 + (u - 4) / 3 : 6 + (u - 16) / 2);
+  };
+  auto rescale_o = [&]() {
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc_o[t] *= alpha;
+  };
+
+  // LDS tile buffers rotate through wrapping byte offsets (not it % n, which
+  // loop strength reduction turns into one address register per read)
+  auto next_buf = [](int off, int n) { return off + TILE == n * TILE ? 0 : off + TILE; };
+
+  // ---- first tile: scores and P only ----
+  if (n_iter > 0) {
+    load_tile(0, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (n_iter > 1) load_tile(1, TILE, TILE);
+    f32x16 s0, s1;
+    qk(sm.k[0], s0, s1);
+    mask(0, s0, s1);
+#pragma unroll
+    for (int u = 0; u < 20; ++u) run_unit(u, s0, s1);  // O is still zero: no scaling due
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pprev[0][i] = pnew[0][i];
+      pprev[1][i] = pnew[1][i];
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile 1 have landed
+    __syncthreads();
+  }
+
+  // ---- steady state: QK of tile it; then the PV product of tile it-1 on the
+  //      matrix cores interleaved with tile it's softmax on the VALU ----
+  // byte offsets of K tile it, V tile it-1 and V tile it+1 in their buffers
+  int kcur = TILE, vprev = 0, vnext = 2 * TILE;
+  for (int it = 1; it < n_iter; ++it) {
+    const int kbase = it * BN;
+    if (it + 1 < n_iter) load_tile(it + 1, next_buf(kcur, KBUF), vnext);
+    f32x16 s0, s1;
+    qk(sm.k[0] + kcur, s0, s1);
+    mask(kbase, s0, s1);
+    // a maximum raised by tile it-1 scales O before tile it-1's product
+    if (grow) rescale_o();
+
+    // issue order, fenced: V reads VPF products ahead; each product followed
+    // by its share of the VALU work (row max first, then the exponentials)
+    const char* vt = sm.v[0] + vprev;
+    u32x4 va[NJ];
+#pragma unroll
+    for (int j = 0; j < VPF; ++j) va[j] = pv_read(vt, j);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if (j + VPF < NJ) va[j + VPF] = pv_read(vt, j + VPF);
+      pv_mfma(j, va[j]);
+#pragma unroll
+      for (int u = 0; u < 20; ++u)
+        if (unit_slot(u) == j) run_unit(u, s0, s1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pin(pnew[0][i]);
+      pin(pnew[1][i]);
+      pprev[0][i] = pnew[0][i];
+      pprev[1][i] = pnew[1][i];
+    }
+    pin(l_run);
+    pin(l_run2);
+    kcur = next_buf(kcur, KBUF);
+    vprev = next_buf(vprev, VBUF);
+    vnext = next_buf(vnext, VBUF);
 
     __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile it+1 have landed
     __syncthreads();
   }
-  if (prev_act0) pv(prev_buf, prev_act1);
+  if (n_iter > 0) {
+    if (grow) rescale_o();
+    const char* vt = sm.v[0] + vprev;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) pv_mfma(j, pv_read(vt, j));
+  }
 
   // ---- epilogue ----
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  l_run += l_run2;
+  const float l_tot = l_run + other_half(l_run);
   if (qrow < nq) {
     const float inv = 1.0f / l_tot;
     bf16* orow = o + ((long)bh * nq + qrow) * D;
