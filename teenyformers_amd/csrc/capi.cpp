@@ -199,6 +199,10 @@ int fa2_check(const void* q, const void* k, const void* v, int n_ctx_q, int n_ct
       (long)batch * hkv * n_ctx_k * head_dim >= kMaxElems)
     return TEENY_ERR_INVALID_SHAPE;
   if (!fa2_head_dim_ok(head_dim, dtype)) return TEENY_ERR_UNSUPPORTED;
+  // bf16 kernels address one head's K / V through a buffer descriptor whose
+  // byte range is a signed 32-bit kernel argument
+  if (dtype == TEENY_BF16 && (long)n_ctx_k * head_dim * 2 >= kMaxElems)
+    return TEENY_ERR_INVALID_SHAPE;
   return TEENY_OK;
 }
 
@@ -213,6 +217,7 @@ int fa2_fwd(bool causal, const void* q, const void* k, const void* v, void* o, f
   char name[64];
   const char* cz = causal ? "c" : "n";
   if (dtype == TEENY_BF16) {
+    // one workgroup of 4 wavefronts per 128 query rows of a (b, head)
     int nmb = (n_ctx_q + 127) / 128;
     long total = (long)nmb * batch * hq;
     if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;

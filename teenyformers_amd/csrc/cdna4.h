@@ -1,0 +1,88 @@
+// gfx950 building blocks shared by the bf16 attention kernels: the 32x32x16
+// bf16 MFMA, LDS transpose reads, buffer-to-LDS DMA, tile swizzles and a few
+// single-instruction helpers.
+#pragma once
+#include "common.h"
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+DEVI float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+DEVI bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+DEVI f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// max of three floats in one instruction.  fmaxf on MFMA results costs an
+// extra canonicalising v_max per operand; scores are never signalling NaNs.
+DEVI float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// the value held by lane l ^ 32 (v_permlane32_swap)
+DEVI float other_half(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
+                                            __builtin_bit_cast(unsigned, x), false, false);
+  // lanes < 32 see (x[l], x[l+32]), lanes >= 32 see (x[l-32], x[l])
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+// acc + lo + hi of a packed bf16 pair (v_dot2c_f32_bf16 against (1, 1))
+DEVI float add_bf16x2(uint32_t w, float acc) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, w),
+                                         __builtin_bit_cast(b2, 0x3f803f80u), acc, false);
+}
+
+// Instruction classes of __builtin_amdgcn_sched_group_barrier: the machine
+// scheduler fills the groups in the order they are declared.
+constexpr int kMfma = 0x008, kDsRead = 0x100;
+#define sched_group(mask, n) __builtin_amdgcn_sched_group_barrier((mask), (n), 0)
+// Keeps the computation of x above this point: values used only in the next
+// loop iteration would otherwise be sunk below the barrier that ends one,
+// out of the block they are scheduled in.
+template <typename T> DEVI void pin(T& x) { asm volatile("" : "+v"(x)); }
+
+// ds_read_b64_tr_b16: within each 16-lane group, output lane i receives
+// element (i % 4) of the 8-byte chunks addressed by lanes i/4, i/4+4, i/4+8
+// and i/4+12 (measured on gfx950): lanes addressing a 4-row x 16-column block
+// of a row-major tile receive it transposed, one column per lane.
+DEVI u32x2 lds_read_tr(const char* p) {
+  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// Raw buffer descriptor (stride 0, num_records in bytes) over [base, +bytes).
+DEVI __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+// buffer_load_dwordx4 ... lds: 16 bytes per lane from buffer offset
+// soff + voff into LDS at lds + 16 * lane.  A MUBUF load, not FLAT: with FLAT
+// LDS loads in flight the compiler waits for every LDS read to drain.
+DEVI void dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, soff, 0, 0);
+}
+
+// Tiles are stored unpadded: 16-byte chunk L = row * (D/8) + column chunk,
+// XOR-swizzled within each 256-byte line (64 banks x 4 bytes); the position
+// of L is swz(L) (an involution).
+//   SWZ_ROW  (read by rows, 16 bytes per lane): position ^= line % 16.
+//   SWZ_DUAL (read by rows and by 4-row transpose reads): position ^= a
+//            bijection of the row's low four bits whose top two bits are the
+//            row's lowest two, so 16 consecutive rows of a row read and the
+//            4 rows x 4 chunks of a transpose-read half-wave touch distinct
+//            banks.  D = 128: x = (r&3)<<2 | (r>>2)&3 (one row per line);
+//            D = 64: two rows per line, x = (line&1)<<2 | (line>>1)&3.
+// Both repeat every 16 rows for D in {64, 128} and every 256 chunks.
+enum Swz { SWZ_ROW, SWZ_DUAL, SWZ_TR8 };
+template <Swz S, int D>
+DEVI int swz(int L) {
+  const int line = L >> 4, pos = L & 15;
+  int x;
+  if (S == SWZ_ROW) x = line & 15;
+  else if (S == SWZ_TR8) x = (line & 3) << 1;
+  else if (D == 128) x = ((line & 3) << 2) | ((line >> 2) & 3);
+  else x = ((line & 1) << 2) | ((line >> 1) & 3);
+  return (line << 4) | (pos ^ x);
+}

@@ -25,7 +25,7 @@
 // LDS, fp32 atomics or a dQ accumulator in HBM.
 // Causal: blocks entirely above the diagonal are skipped, diagonal blocks
 // are masked.
-#include "common.h"
+#include "cdna4.h"
 
 namespace {
 
@@ -35,23 +35,6 @@ constexpr int KPAD = 8;   // rows read only row-wise: stride = 4 mod 64 dwords
 constexpr int QPAD = 24;  // rows read row-wise and transposed: stride = 12 mod 64 dwords (D=128)
 constexpr float kLog2e = 1.4426950408889634f;
 
-DEVI float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-DEVI bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-DEVI f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-// ds_read_b64_tr_b16: within each 16-lane group, output lane i receives
-// element (i % 4) of the 8-byte chunks addressed by lanes i/4, i/4+4, i/4+8
-// and i/4+12 (measured on gfx950): lanes addressing a 4-row x 16-column block
-// of a row-major tile receive it transposed, one column per lane.
-DEVI u32x2 lds_read_tr(const bf16* p) {
-  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4*)(p));
-  return __builtin_bit_cast(u32x2, r);
-}
 
 // A operand X^T of v_mfma_f32_32x32x16_bf16 (M = columns of X, K = rows of
 // X) from a row-major LDS tile X whose rows hold the summation index:
@@ -63,8 +46,8 @@ DEVI bf16x8 xt_operand(const bf16* tile, int r0, int c0, int lane) {
   const int g = lane >> 5;
   const bf16* p = tile + (r0 + 4 * g + ((lane & 15) >> 2)) * STRIDE + c0 +
                   16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  u32x2 a0 = lds_read_tr(p);
-  u32x2 a1 = lds_read_tr(p + 8 * STRIDE);
+  u32x2 a0 = lds_read_tr(reinterpret_cast<const char*>(p));
+  u32x2 a1 = lds_read_tr(reinterpret_cast<const char*>(p + 8 * STRIDE));
   return as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
 }
 
@@ -292,12 +275,14 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
 // dQ (query-parallel)
 // ===========================================================================
 constexpr int QBM = 128;  // query rows per workgroup (4 waves x 32)
-constexpr int QBN = 32;   // keys per iteration
+constexpr int QBN = 64;   // keys per LDS tile, processed as two 32-key halves
+constexpr int QKBUF = 3;  // K tiles: previous (its transpose is still read), current, loading
+constexpr int QVBUF = 2;  // V tiles: current, loading
 
 template <int D>
 struct __attribute__((aligned(16))) DqSmem {
-  bf16 k[2][QBN][D + QPAD];  // K tile: A operand of S^T, transposed A operand of dQ^T
-  bf16 v[2][QBN][D + KPAD];  // V tile: A operand of dP^T
+  char k[QKBUF][QBN * D * 2];
+  char v[QVBUF][QBN * D * 2];
 };
 
 template <int D, bool CAUSAL>
@@ -309,10 +294,14 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   constexpr int DC = D / 16;
   constexpr int DT = D / 32;
   constexpr int CPR = D / 8;
+  constexpr int TILE = QBN * D * 2;    // bytes per tile
+  constexpr int HALF = 32 * D * 2;     // bytes of 32 rows
+  constexpr int TCH = QBN * CPR / 256; // 16-byte chunks per thread per tile
   __shared__ DqSmem<D> sm;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  // wave-uniform (an SGPR): every branch on it is a scalar branch
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
 
   const int id = xcd_remap(blockIdx.x, total_blocks);
@@ -322,22 +311,22 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   const long kvh = (long)b * hkv + h / (hq / hkv);
   const int m0 = mb * QBM;
   const int qrow = m0 + wave * 32 + l32;
-  const int wave_qmax = m0 + wave * 32 + 31;
   const bool qok = qrow < nq;
 
   const bf16* kb = k + kvh * (long)nk * D;
   const bf16* vb = v + kvh * (long)nk * D;
 
   // ---- this lane's Q and dO row (B operands), LSE and Delta ----------------
+  // rows past nq load row nq - 1 and get LSE = +inf (P = 0): never stored
   bf16x8 qreg[DC], doreg[DC];
   {
-    const long row = (long)bh * nq + (qok ? qrow : 0);
+    const long row = (long)bh * nq + min(qrow, nq - 1);
     const bf16* qp = q + row * D + 8 * g;
     const bf16* dp = dout + row * D + 8 * g;
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
-      qreg[c] = as_bf16x8(qok ? *reinterpret_cast<const u32x4*>(qp + 16 * c) : u32x4{0, 0, 0, 0});
-      doreg[c] = as_bf16x8(qok ? *reinterpret_cast<const u32x4*>(dp + 16 * c) : u32x4{0, 0, 0, 0});
+      qreg[c] = as_bf16x8(*reinterpret_cast<const u32x4*>(qp + 16 * c));
+      doreg[c] = as_bf16x8(*reinterpret_cast<const u32x4*>(dp + 16 * c));
     }
   }
   const float lse2 = qok ? lse[(long)bh * nq + qrow] * kLog2e : INFINITY;
@@ -348,81 +337,169 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   if (CAUSAL) kend = min(nk, m0 + QBM);
   const int n_iter = (kend + QBN - 1) / QBN;
 
-  // Staging: a K or V tile is QBN x CPR 16-byte chunks; each thread carries
-  // TCH chunks of both.
-  constexpr int TCH = QBN * CPR / 256;
-  u32x4 kstage[TCH], vstage[TCH];
-  auto load_tile = [&](int kbase) {
+  // ---- K / V tiles: buffer_load ... lds, both SWZ_DUAL ----------------------
+  const uint32_t src = swz<SWZ_DUAL, D>(wave * 64 + lane) * 16;
+  const auto krsrc = make_rsrc(kb, nk * D * 2);
+  const auto vrsrc = make_rsrc(vb, nk * D * 2);
+  auto load_tile = [&](int it, int koff, int voff) {
+    const int kbase = it * QBN;
+    char* kdst = sm.k[0] + koff + wave * 64 * 16;
+    char* vdst = sm.v[0] + voff + wave * 64 * 16;
+    const int sbase = kbase * D * 2;
+    if (kbase + QBN <= nk) {
 #pragma unroll
-    for (int i = 0; i < TCH; ++i) {
-      const int c = i * 256 + tid;
-      const int key = kbase + c / CPR;
-      const long off = (long)key * D + (c % CPR) * 8;
-      kstage[i] = key < nk ? *reinterpret_cast<const u32x4*>(kb + off) : u32x4{0, 0, 0, 0};
-      vstage[i] = key < nk ? *reinterpret_cast<const u32x4*>(vb + off) : u32x4{0, 0, 0, 0};
+      for (int i = 0; i < TCH; ++i) {
+        dma16(krsrc, kdst + i * 4096, src, sbase + i * 4096);
+        dma16(vrsrc, vdst + i * 4096, src, sbase + i * 4096);
+      }
+    } else {  // rows past the sequence re-read its last row (masked later)
+      const int last = nk - 1 - kbase;
+#pragma unroll
+      for (int i = 0; i < TCH; ++i) {
+        const int o = i * 4096 + src;
+        const int oc = min(o / (2 * D), last) * (2 * D) + o % (2 * D);
+        dma16(krsrc, kdst + i * 4096, oc, sbase);
+        dma16(vrsrc, vdst + i * 4096, oc, sbase);
+      }
     }
   };
-  auto store_tile = [&](int buf) {
+  auto next_buf = [](int off, int n) { return off + TILE == n * TILE ? 0 : off + TILE; };
+
+  // ---- LDS read offsets (bytes) --------------------------------------------
+  // rows: lane reads row l32 (+32 per half), column chunk 2c + g
+  int row_off[DC];
 #pragma unroll
-    for (int i = 0; i < TCH; ++i) {
-      const int c = i * 256 + tid;
-      *reinterpret_cast<u32x4*>(&sm.k[buf][c / CPR][(c % CPR) * 8]) = kstage[i];
-      *reinterpret_cast<u32x4*>(&sm.v[buf][c / CPR][(c % CPR) * 8]) = vstage[i];
+  for (int c = 0; c < DC; ++c) row_off[c] = swz<SWZ_DUAL, D>(l32 * CPR + 2 * c + g) * 16;
+  // K^T (transpose reads): lane p of 16-lane group G reads row 8e + 4g + p/4
+  // (+16 hh, +32 per half: the swizzle repeats every 16 rows) and 8 bytes at
+  // column 32t + 16(G%2) + 4(p%4)
+  int tr_off[DT][2];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int row = 8 * e + 4 * g + ((lane & 15) >> 2);
+      const int col = 32 * t + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+      tr_off[t][e] = swz<SWZ_DUAL, D>(row * CPR + col / 8) * 16 + (col % 8) * 2;
     }
-  };
 
   f32x16 acc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
+  // dS^T of the previous 32-key half (B operand of its delayed dQ^T product)
+  uint32_t dsb_prev[8], dsb_new[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dsb_prev[i] = 0;
 
-  if (n_iter > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int it = 0; it < n_iter; ++it) {
-    const int cur = it & 1;
-    const int kbase = it * QBN;
-    if (it + 1 < n_iter) load_tile(kbase + QBN);
-    if (!(CAUSAL && kbase > wave_qmax)) {
-      // S^T = K Q^T, dP^T = V dO^T: lane = query row, 16 keys.
-      f32x16 s = f32x16{}, dp = f32x16{};
-      const bf16* krow = &sm.k[cur][l32][8 * g];
-      const bf16* vrow = &sm.v[cur][l32][8 * g];
+  // S^T = K Q^T and dP^T = V dO^T for 32 keys (lane = query row, 16 keys),
+  // fragments read KPF steps ahead
+  auto s_dp = [&](const char* kt, const char* vt, f32x16& s, f32x16& dp) {
+    constexpr int KPF = 2;
+    s = f32x16{};
+    dp = f32x16{};
+    u32x4 ak[DC], av[DC];
 #pragma unroll
-      for (int c = 0; c < DC; ++c) {
-        u32x4 ak = *reinterpret_cast<const u32x4*>(krow + 16 * c);
-        s = mfma32(as_bf16x8(ak), qreg[c], s);
-        u32x4 av = *reinterpret_cast<const u32x4*>(vrow + 16 * c);
-        dp = mfma32(as_bf16x8(av), doreg[c], dp);
+    for (int c = 0; c < KPF; ++c) {
+      ak[c] = *reinterpret_cast<const u32x4*>(kt + row_off[c]);
+      av[c] = *reinterpret_cast<const u32x4*>(vt + row_off[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      if (c + KPF < DC) {
+        ak[c + KPF] = *reinterpret_cast<const u32x4*>(kt + row_off[c + KPF]);
+        av[c + KPF] = *reinterpret_cast<const u32x4*>(vt + row_off[c + KPF]);
       }
-      const bool need_mask = (kbase + QBN > nk) || (CAUSAL && kbase + QBN - 1 > m0 + wave * 32);
-      uint32_t dsb[8];
+      s = mfma32(as_bf16x8(ak[c]), qreg[c], s);
+      dp = mfma32(as_bf16x8(av[c]), doreg[c], dp);
+    }
+    sched_group(kDsRead, 2 * KPF);
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        float p0 = fast_exp2(__builtin_fmaf(s[r], sl2, -lse2));
-        float p1 = fast_exp2(__builtin_fmaf(s[r + 1], sl2, -lse2));
-        if (need_mask) {
-          int key = kbase + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key >= nk || (CAUSAL && key > qrow)) p0 = 0.0f;
-          if (key + 1 >= nk || (CAUSAL && key + 1 > qrow)) p1 = 0.0f;
-        }
-        dsb[r >> 1] = pack_bf16x2(p0 * (dp[r] - dlt), p1 * (dp[r + 1] - dlt));
-      }
-      // dQ^T += K^T dS^T
+    for (int c = 0; c < DC; ++c) {
+      if (c + KPF < DC) sched_group(kDsRead, 2);
+      sched_group(kMfma, 2);
+    }
+  };
+  // keys past nk or (causal) past the row -> score -inf, so P = dS = 0
+  auto mask = [&](int kb0, f32x16& s) {
+    if ((kb0 + 32 > nk) || (CAUSAL && kb0 + 31 > m0 + wave * 32)) {
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        bf16x8 bop =
-            as_bf16x8(u32x4{dsb[4 * hh], dsb[4 * hh + 1], dsb[4 * hh + 2], dsb[4 * hh + 3]});
-#pragma unroll
-        for (int t = 0; t < DT; ++t)
-          acc[t] = mfma32(xt_operand<D + QPAD>(&sm.k[cur][0][0], 16 * hh, 32 * t, lane), bop,
-                          acc[t]);
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb0 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (key >= nk || (CAUSAL && key > qrow)) s[r] = -INFINITY;
       }
     }
-    if (it + 1 < n_iter) store_tile(cur ^ 1);
+  };
+  // dQ^T += K^T dS^T, product j = (hh, t): keys 16hh.. of a half, d-tile t
+  constexpr int NJ = 2 * DT;
+  auto dq_read = [&](const char* kt, int j) {
+    const int t = j % DT, hh = j / DT;
+    const char* p = kt + hh * 16 * D * 2;
+    u32x2 a0 = lds_read_tr(p + tr_off[t][0]), a1 = lds_read_tr(p + tr_off[t][1]);
+    return u32x4{a0[0], a0[1], a1[0], a1[1]};
+  };
+  auto dq_mfma = [&](int j, u32x4 a) {
+    const int t = j % DT, hh = j / DT;
+    bf16x8 bop = as_bf16x8(
+        u32x4{dsb_prev[4 * hh], dsb_prev[4 * hh + 1], dsb_prev[4 * hh + 2], dsb_prev[4 * hh + 3]});
+    acc[t] = mfma32(as_bf16x8(a), bop, acc[t]);
+  };
+  // P and dS = P (dP - Delta) for score pair r, r+1 -> packed bf16
+  auto ds_pair = [&](const f32x16& s, const f32x16& dp, int r) {
+    const float p0 = fast_exp2(__builtin_fmaf(s[r], sl2, -lse2));
+    const float p1 = fast_exp2(__builtin_fmaf(s[r + 1], sl2, -lse2));
+    dsb_new[r >> 1] = pack_bf16x2(p0 * (dp[r] - dlt), p1 * (dp[r + 1] - dlt));
+  };
+  // the previous half's dQ^T product on the matrix cores, interleaved with
+  // this half's exponentials on the VALU (issue order fenced)
+  auto dq_and_ds = [&](const char* kprev, const f32x16& s, const f32x16& dp) {
+    constexpr int VPF = 2;
+    constexpr int PPJ = 8 / NJ;  // pairs per product
+    u32x4 va[NJ];
+#pragma unroll
+    for (int j = 0; j < VPF; ++j) va[j] = dq_read(kprev, j);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if (j + VPF < NJ) va[j + VPF] = dq_read(kprev, j + VPF);
+      dq_mfma(j, va[j]);
+#pragma unroll
+      for (int i = 0; i < PPJ; ++i) ds_pair(s, dp, 2 * (j * PPJ + i));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pin(dsb_new[i]);
+      dsb_prev[i] = dsb_new[i];
+    }
+  };
+
+  // The first lagged product reads the K half "before" tile 0 with dS = 0:
+  // zero it (buffer QKBUF-1, second half) so that 0 * K stays 0.
+  for (int i = tid; i < HALF / 16; i += 256)
+    *reinterpret_cast<u32x4*>(sm.k[QKBUF - 1] + HALF + 16 * i) = u32x4{0, 0, 0, 0};
+  if (n_iter > 0) load_tile(0, 0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  int kcur = 0, vcur = 0;                     // byte offsets of tile it's buffers
+  int kprev = (QKBUF - 1) * TILE + HALF;      // K half whose dS^T is pending
+  for (int it = 0; it < n_iter; ++it) {
+    if (it + 1 < n_iter) load_tile(it + 1, next_buf(kcur, QKBUF), next_buf(vcur, QVBUF));
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      f32x16 s, dp;
+      s_dp(sm.k[0] + kcur + u * HALF, sm.v[0] + vcur + u * HALF, s, dp);
+      mask(it * QBN + 32 * u, s);
+      dq_and_ds(sm.k[0] + kprev, s, dp);
+      kprev = kcur + u * HALF;
+    }
+    kcur = next_buf(kcur, QKBUF);
+    vcur = next_buf(vcur, QVBUF);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile it+1 have landed
     __syncthreads();
+  }
+  if (n_iter > 0) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) dq_mfma(j, dq_read(sm.k[0] + kprev, j));
   }
 
   if (qok) {

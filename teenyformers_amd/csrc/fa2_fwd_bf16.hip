@@ -7,25 +7,35 @@
 // query row; this kernel keeps bf16 operands with fp32 accumulation and a
 // fp32 online softmax.
 //
-// Tiling (one workgroup = 4 wavefronts = 128 query rows of one (b, h)):
+// Tiling (one workgroup = 4 wavefronts = 128 query rows of one (b, h); two
+// workgroups per CU, so the two waves on each SIMD run independently and
+// cover each other's MFMA / VALU phases):
 //   * each wave owns 32 query rows; its Q rows live in registers as the
 //     B operand of v_mfma_f32_32x32x16_bf16;
-//   * K/V advance in tiles of 64 keys, double-buffered in LDS, both stored
-//     row-major [key][d]; K is read as an A operand with 16-byte reads, V^T
-//     with the LDS transpose read ds_read_b64_tr_b16 (see vt_operand);
-//   * S^T = K Q^T puts one query row in each lane (lane % 32) and 16 keys per
-//     lane per 32-key subtile, so the row max / row sum are in-lane plus one
+//   * K/V advance in tiles of 64 keys that buffer_load ... lds streams into
+//     LDS one tile ahead (K: 2 buffers, V: 3, since the PV product of a tile
+//     runs one iteration late); K is stored SWZ_ROW and read row-wise as the
+//     A operand of S^T = K Q^T, V is stored SWZ_DUAL and read with the LDS
+//     transpose read ds_read_b64_tr_b16 as the A operand of O^T += V^T P^T
+//     (both bank-conflict free);
+//   * S^T puts one query row in each lane (lane % 32) and 16 keys per lane
+//     per 32-key subtile, so the row max / row sum are in-lane plus one
 //     exchange between the two lane halves;
 //   * the fp32 accumulator of S^T, rounded to bf16, is already in the
 //     B-operand layout of O^T += V^T P^T (keys are a summation index, so the
 //     key order inside each 16-key chunk only has to agree between A and B);
-//   * causal: key tiles past the block's last query row are skipped, subtiles
-//     past a wave's last row are skipped, only diagonal tiles are masked;
+//   * the PV product of tile i-1 is issued one MFMA at a time between the
+//     row max and exponentials of tile i (fenced issue order), so the matrix
+//     cores and the VALU work at once within one wave;
+//   * online softmax in the log2 domain (exp2 with log2(e) folded into the
+//     scale) with a lazy, branch-free maximum update: O is rescaled only when
+//     some row's maximum grew by more than 2^8;
+//   * causal: key tiles past the block's last row are not loaded, diagonal
+//     tiles are masked;
 //   * GQA: q head h reads kv head h / (Hq / Hkv);
 //   * scheduling: block ids are remapped so one XCD works through whole heads
 //     (K/V stay in that XCD's L2), heaviest causal blocks first.
-// exp is exp2 with log2(e) folded into the scale (v_exp_f32).
-#include "common.h"
+#include "cdna4.h"
 
 namespace {
 
@@ -36,76 +46,6 @@ constexpr int VBUF = 3;  // V tiles: read by PV(i-1), waiting (i), loading (i+1)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescale = 8.0f;  // lazy-rescale threshold, log2 units
-
-DEVI float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-// max of three floats in one instruction.  fmaxf on MFMA results costs an
-// extra canonicalising v_max per operand; scores are never signalling NaNs.
-DEVI float max3(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
-// (value in lane l, value in lane l ^ 32) via v_permlane32_swap
-DEVI float other_half(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
-                                            __builtin_bit_cast(unsigned, x), false, false);
-  // lanes < 32 see (x[l], x[l+32]), lanes >= 32 see (x[l-32], x[l])
-  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
-}
-// acc + lo + hi of a packed bf16 pair (v_dot2c_f32_bf16 against (1, 1))
-DEVI float add_bf16x2(uint32_t w, float acc) {
-  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, w),
-                                         __builtin_bit_cast(b2, 0x3f803f80u), acc, false);
-}
-DEVI bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-DEVI f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-// Instruction classes of __builtin_amdgcn_sched_group_barrier: the machine
-// scheduler fills the groups in the order they are declared.
-constexpr int kMfma = 0x008, kDsRead = 0x100;
-#define sched_group(mask, n) __builtin_amdgcn_sched_group_barrier((mask), (n), 0)
-// Keeps the computation of x above this point: values used only in the next
-// loop iteration would otherwise be sunk below the barrier that ends one,
-// out of the block they are scheduled in.
-template <typename T> DEVI void pin(T& x) { asm volatile("" : "+v"(x)); }
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Raw buffer descriptor (stride 0, num_records in bytes) over [base, +bytes).
-DEVI __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
-}
-// 16 bytes per lane from buffer offset soff + voff into LDS at lds + 16 * lane
-DEVI void dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voff, int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, soff, 0, 0);
-}
-
-// ds_read_b64_tr_b16: within each 16-lane group, output lane i receives
-// element (i % 4) of the 8-byte chunks addressed by lanes i/4, i/4+4, i/4+8
-// and i/4+12 (measured on gfx950): lanes addressing a 4-row x 16-column block
-// of a row-major tile receive it transposed, one column per lane.
-DEVI u32x2 lds_read_tr(const char* p) {
-  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4*)(p));
-  return __builtin_bit_cast(u32x2, r);
-}
-
-// Tiles are stored unpadded, 16-byte chunk L = row * (D/8) + column-chunk,
-// and XOR-swizzled within each 256-byte line (64 banks x 4 bytes):
-//   K (read by rows, 16 bytes per lane):   position ^= line % 16
-//   V (read by the 4-row transpose reads): position ^= 2 * (line % 4)
-// so 16 lanes of either read touch distinct bank groups, and both swizzles
-// repeat every 8 rows for D = 64 and D = 128 (the reads step by 8 rows).
-template <bool VLAYOUT>
-DEVI int swz_chunk(int L) {
-  const int line = L >> 4, pos = L & 15;
-  const int x = VLAYOUT ? ((line & 3) << 1) : (line & 15);
-  return (line << 4) | (pos ^ x);
-}
 
 template <int D>
 struct __attribute__((aligned(16))) FwdSmem {
@@ -162,8 +102,8 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   // (i*256 + wave*64 + lane) of the tile; each lane fetches the tile chunk
   // that the swizzle puts there.  Adding 256 chunks (16 lines) leaves both
   // swizzles unchanged, so a lane's chunks are one byte offset plus i * 4096.
-  const uint32_t k_src = swz_chunk<false>(wave * 64 + lane) * 16;
-  const uint32_t v_src = swz_chunk<true>(wave * 64 + lane) * 16;
+  const uint32_t k_src = swz<SWZ_ROW, D>(wave * 64 + lane) * 16;
+  const uint32_t v_src = swz<SWZ_DUAL, D>(wave * 64 + lane) * 16;
   const auto krsrc = make_rsrc(kb, nk * D * 2);
   const auto vrsrc = make_rsrc(vb, nk * D * 2);
   // it: tile index; koff / voff: byte offsets of its K and V buffers
@@ -193,17 +133,20 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   // K: lane reads row 32*kt + l32, column chunk 2c + g.
   int k_off[DC];
 #pragma unroll
-  for (int c = 0; c < DC; ++c) k_off[c] = swz_chunk<false>(l32 * CPR + 2 * c + g) * 16;
+  for (int c = 0; c < DC; ++c) k_off[c] = swz<SWZ_ROW, D>(l32 * CPR + 2 * c + g) * 16;
   // V^T: lane p of 16-lane group G reads row 4g + p/4 (+8, +16hh, +32kt) and
   // 8 bytes at column 32t + 16(G%2) + 4(p%4); rows differing by 8 share the
   // swizzle, so only the column tile t needs its own offset.
   const int vr = 4 * g + ((lane & 15) >> 2);
-  int v_off[DT];
+  int v_off[DT][2];
 #pragma unroll
-  for (int t = 0; t < DT; ++t) {
-    const int col = 32 * t + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    v_off[t] = swz_chunk<true>(vr * CPR + col / 8) * 16 + (col % 8) * 2;
-  }
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int row = 8 * e + 4 * g + ((lane & 15) >> 2);
+      const int col = 32 * t + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+      v_off[t][e] = swz<SWZ_DUAL, D>(row * CPR + col / 8) * 16 + (col % 8) * 2;
+    }
   constexpr int ROW8 = 8 * D * 2;  // bytes of 8 rows (a swizzle-invariant step)
 
   // ---- running state ---------------------------------------------------------
@@ -228,8 +171,8 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   constexpr int VPF = 2;  // V fragments are read this many products ahead
   auto pv_read = [&](const char* vt, int j) {
     const int t = j % DT, hh = (j / DT) & 1, kt = j / (2 * DT);
-    const char* p = vt + v_off[t] + (4 * kt + 2 * hh) * ROW8;
-    u32x2 a0 = lds_read_tr(p), a1 = lds_read_tr(p + ROW8);
+    const char* p = vt + (4 * kt + 2 * hh) * ROW8;
+    u32x2 a0 = lds_read_tr(p + v_off[t][0]), a1 = lds_read_tr(p + v_off[t][1]);
     return u32x4{a0[0], a0[1], a1[0], a1[1]};
   };
   auto pv_mfma = [&](int j, u32x4 a) {
