@@ -110,7 +110,9 @@ int teeny_flash_attn2_bwd(const void* q, const void* k, const void* v, const voi
                           int n_heads_kv, int head_dim, int dtype, void* workspace,
                           size_t workspace_bytes, hipStream_t stream);
 
-/* Workspace the backward needs: Delta = rowsum(O * dO) [B*Hq, n_ctx_q] fp32.
+/* Workspace the backward needs.  bf16: per (b, q head) and block of 32 query
+ * rows, 32 values of LSE*log2(e) followed by 32 of Delta = rowsum(O * dO),
+ * fp32, the last block padded; fp32: Delta [B*Hq, n_ctx_q].
  * No counterpart in the reference
  * (its executor sizes caches from RuntimeOp::param_shapes, flash_attn2.rs:449-457). */
 size_t teeny_flash_attn2_bwd_workspace_bytes(int n_ctx_q, int batch, int n_heads_q, int head_dim,

@@ -231,10 +231,16 @@ int fa2_fwd(bool causal, const void* q, const void* k, const void* v, void* o, f
   return launch(name, dim3((n_ctx_q + 63) / 64, batch * hq), dim3(64), 0, stream, args);
 }
 
+// bf16: per (b, q head) and block of 32 query rows, 32 values of LSE*log2(e)
+// then 32 of Delta (fp32; the last block padded).  fp32: Delta [B*Hq, n_ctx_q].
+constexpr int kLdRows = 32;
 size_t fa2_bwd_ws(int n_ctx_q, int batch, int hq, int head_dim, int dtype) {
   (void)head_dim;
-  (void)dtype;
-  return align256((size_t)batch * hq * n_ctx_q * sizeof(float));  // Delta
+  if (dtype == TEENY_BF16) {
+    const size_t nq_pad = (size_t)(n_ctx_q + kLdRows - 1) / kLdRows * kLdRows;
+    return align256((size_t)batch * hq * nq_pad * 2 * sizeof(float));
+  }
+  return align256((size_t)batch * hq * n_ctx_q * sizeof(float));
 }
 
 int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void* o,
@@ -252,10 +258,12 @@ int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void
   const char* cz = causal ? "c" : "n";
   char name[64];
   if (dtype == TEENY_BF16) {
+    float* ld = (float*)workspace;
+    const long prows = (long)batch * hq * ((n_ctx_q + kLdRows - 1) / kLdRows * kLdRows);
     const int rows_per_block = 256 / (head_dim / 8);
     snprintf(name, sizeof name, "teeny_fa2_bwd_pre_bf16_d%d", head_dim);
-    void* a0[] = {&o, &dout, &delta, (void*)&rows};
-    rc = launch(name, dim3((unsigned)((rows + rows_per_block - 1) / rows_per_block)), dim3(256),
+    void* a0[] = {&o, &dout, &l, &ld, &n_ctx_q, (void*)&prows};
+    rc = launch(name, dim3((unsigned)((prows + rows_per_block - 1) / rows_per_block)), dim3(256),
                 0, stream, a0);
     if (rc) return rc;
     // dK, dV: one workgroup per 128 keys of a (b, kv head)
@@ -264,8 +272,8 @@ int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void
     if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
     int tot = (int)total;
     snprintf(name, sizeof name, "teeny_fa2_bwd_dkdv_bf16_d%d_%s", head_dim, cz);
-    void* a1[] = {&q,       &k,       &v,     &dout, &l,   &delta, &dk,  &dv,
-                  &n_ctx_q, &n_ctx_k, &scale, &hq,   &hkv, &nnb,   &tot};
+    void* a1[] = {&q,       &k,       &v,     &dout, &ld,  &dk,  &dv,
+                  &n_ctx_q, &n_ctx_k, &scale, &hq,   &hkv, &nnb, &tot};
     rc = launch(name, dim3(tot), dim3(256), 0, stream, a1);
     if (rc) return rc;
     // dQ: one workgroup per 128 query rows of a (b, q head)
@@ -274,8 +282,8 @@ int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void
     if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
     tot = (int)total;
     snprintf(name, sizeof name, "teeny_fa2_bwd_dq_bf16_d%d_%s", head_dim, cz);
-    void* a2[] = {&q,       &k,       &v,     &dout, &l,   &delta, &dq,
-                  &n_ctx_q, &n_ctx_k, &scale, &hq,   &hkv, &nmb,   &tot};
+    void* a2[] = {&q,     &k,   &v,   &dout, &ld,  &dq, &n_ctx_q,
+                  &n_ctx_k, &scale, &hq, &hkv, &nmb, &tot};
     return launch(name, dim3(tot), dim3(256), 0, stream, a2);
   }
   snprintf(name, sizeof name, "teeny_fa2_bwd_pre_f32_d%d", head_dim);

@@ -8,18 +8,21 @@
 // The reference runs one CTA per query row and adds dK/dV with fp32 atomics
 // (nondeterministic).  Here the backward is three kernels, all deterministic
 // and free of atomics:
-//   1. bwd_pre: Delta = rowsum(O o dO) in fp32;
+//   1. bwd_pre: per block of 32 query rows, LSE * log2(e) and
+//      Delta = rowsum(O o dO) in fp32 (rows past nq: +inf and 0, so the
+//      padded rows contribute P = 0);
 //   2. dK/dV, key-parallel: one workgroup (4 wavefronts) owns 128 keys of one
-//      (b, kv head); each wave's 32 K rows stay in registers and its V rows in
-//      LDS as B operands of v_mfma_f32_32x32x16_bf16, and it walks the 32-row query
-//      blocks of every q head of its GQA group (Q, dO staged row-major in
-//      double-buffered LDS and read both row-wise and, through the LDS
-//      transpose read, as Q^T / dO^T), accumulating dK^T and dV^T in
-//      registers: the GQA reduction comes for free;
+//      (b, kv head); each wave's 32 K rows stay in registers and the block's
+//      V rows in LDS as B operands of v_mfma_f32_32x32x16_bf16, and it walks
+//      the 32-row query blocks of every q head of its GQA group (Q, dO tiles
+//      streamed into double-buffered LDS by buffer_load ... lds and read both
+//      row-wise and, through the LDS transpose read, as Q^T / dO^T),
+//      accumulating dK^T and dV^T in registers: the GQA reduction comes for
+//      free;
 //   3. dQ, query-parallel, shaped like the forward: each wave's Q and dO
-//      rows are B operands in registers, 32-key tiles of K and V stream
-//      through double-buffered LDS (K^T via the transpose read), S^T and dP^T put one query row
-//      in each lane, and dQ^T += K^T dS^T accumulates in registers.
+//      rows are B operands in registers, 64-key tiles of K and V stream
+//      through LDS (K^T via the transpose read), S^T and dP^T put one query
+//      row in each lane, and dQ^T += K^T dS^T accumulates in registers.
 // Recomputing S and dP in the dQ kernel costs 7 matrix products per tile
 // pair instead of 5; in exchange neither kernel needs dS round trips through
 // LDS, fp32 atomics or a dQ accumulator in HBM.
@@ -30,36 +33,27 @@
 namespace {
 
 constexpr int BN = 128;  // keys per workgroup
-constexpr int BM = 32;   // query rows per iteration
-constexpr int KPAD = 8;   // rows read only row-wise: stride = 4 mod 64 dwords
-constexpr int QPAD = 24;  // rows read row-wise and transposed: stride = 12 mod 64 dwords (D=128)
+constexpr int BM = 32;   // query rows per iteration; also the row block of the LSE / Delta array
 constexpr float kLog2e = 1.4426950408889634f;
 
 
-// A operand X^T of v_mfma_f32_32x32x16_bf16 (M = columns of X, K = rows of
-// X) from a row-major LDS tile X whose rows hold the summation index:
-// lane (l32, g) receives X[r0 + 4g + 0..3][c0 + l32] and
-// X[r0 + 8 + 4g + 0..3][c0 + l32], the row order in which a 32x32 MFMA
-// accumulator holds rows 16hh + 8*(e/4) + 4g + e%4 for its B operand.
-template <int STRIDE>
-DEVI bf16x8 xt_operand(const bf16* tile, int r0, int c0, int lane) {
-  const int g = lane >> 5;
-  const bf16* p = tile + (r0 + 4 * g + ((lane & 15) >> 2)) * STRIDE + c0 +
-                  16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  u32x2 a0 = lds_read_tr(reinterpret_cast<const char*>(p));
-  u32x2 a1 = lds_read_tr(reinterpret_cast<const char*>(p + 8 * STRIDE));
-  return as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
-}
-
-// Delta = rowsum(O o dO) in fp32.
+// Per (b, q head) and block of BM query rows, ld holds BM values of
+// LSE * log2(e) followed by BM values of Delta = rowsum(O o dO), fp32; rows
+// past nq hold +inf and 0.  One thread group of D/8 lanes per (padded) row.
 template <int D>
 __device__ void bwd_pre(const bf16* __restrict__ o, const bf16* __restrict__ dout,
-                        float* __restrict__ delta, long rows) {
+                        const float* __restrict__ lse, float* __restrict__ ld, int nq,
+                        long padded_rows) {
   constexpr int TPR = D / 8;  // threads per row, 8 elements each
-  const long row = (long)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
+  const long prow = (long)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
   const int c = threadIdx.x % TPR;
+  const int nq_pad = (nq + BM - 1) / BM * BM;
+  const long bh = prow / nq_pad;
+  const int i = (int)(prow - bh * nq_pad);
+  const bool ok = prow < padded_rows && i < nq;
   float s = 0.0f;
-  if (row < rows) {
+  if (ok) {
+    const long row = bh * nq + i;
     float a[8], bb[8];
     Vec16<bf16>::load(o + row * D + 8 * c, a);
     Vec16<bf16>::load(dout + row * D + 8 * c, bb);
@@ -68,7 +62,11 @@ __device__ void bwd_pre(const bf16* __restrict__ o, const bf16* __restrict__ dou
   }
 #pragma unroll
   for (int off = TPR / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-  if (row < rows && c == 0) delta[row] = s;
+  if (prow < padded_rows && c == 0) {
+    float* blk = ld + (prow / BM) * (2 * BM);
+    blk[i % BM] = ok ? lse[bh * nq + i] * kLog2e : INFINITY;
+    blk[BM + i % BM] = ok ? s : 0.0f;
+  }
 }
 
 // ===========================================================================
@@ -76,26 +74,28 @@ __device__ void bwd_pre(const bf16* __restrict__ o, const bf16* __restrict__ dou
 // ===========================================================================
 template <int D>
 struct __attribute__((aligned(16))) DkdvSmem {
-  bf16 qs[2][BM][D + QPAD];   // Q tile: A operand of S, transposed A operand of dK^T
-  bf16 dos[2][BM][D + QPAD];  // dO tile: A operand of dP, transposed A operand of dV^T
-  float lse2[2][BM];          // LSE * log2(e); +inf for rows past nq
-  float delta[2][BM];
-  bf16 vs[BN][D + KPAD];      // the block's V rows (B operand of dP)
+  char v[BN * D * 2];     // the block's V rows: B operand of dP
+  char q[2][BM * D * 2];  // Q tile: A operand of S, transposed A operand of dK^T
+  char d[2][BM * D * 2];  // dO tile: A operand of dP, transposed A operand of dV^T
+  float ld[2][2 * BM];    // LSE * log2(e) and Delta of the tile's rows
 };
 
 template <int D, bool CAUSAL>
 __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict__ k,
                              const bf16* __restrict__ v, const bf16* __restrict__ dout,
-                             const float* __restrict__ lse, const float* __restrict__ delta,
-                             bf16* __restrict__ dk, bf16* __restrict__ dv, int nq, int nk,
-                             float scale, int hq, int hkv, int num_n_blocks, int total_blocks) {
-  constexpr int DC = D / 16;  // d-chunks of 16 (QK^T, dO V^T)
-  constexpr int DT = D / 32;  // d-tiles of 32 (dK^T, dV^T)
-  constexpr int CPR = D / 8;  // 16-byte chunks per row
+                             const float* __restrict__ ld, bf16* __restrict__ dk,
+                             bf16* __restrict__ dv, int nq, int nk, float scale, int hq, int hkv,
+                             int num_n_blocks, int total_blocks) {
+  constexpr int DC = D / 16;            // d-chunks of 16 (QK^T, dO V^T)
+  constexpr int DT = D / 32;            // d-tiles of 32 (dK^T, dV^T)
+  constexpr int CPR = D / 8;            // 16-byte chunks per row
+  constexpr int TCH = BM * CPR / 256;   // chunks per thread of a Q or dO tile
+  constexpr int VCH = BN * CPR / 256;   // chunks per thread of the V block
   __shared__ DkdvSmem<D> sm;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  // wave-uniform (an SGPR): every branch on it is a scalar branch
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
 
   const int id = xcd_remap(blockIdx.x, total_blocks);
@@ -106,72 +106,91 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
   const int n0 = nb * BN;
   const int kw0 = n0 + 32 * wave;  // this wave's first key
   const int mykey = kw0 + l32;
+  const int nq_pad = (nq + BM - 1) / BM * BM;
 
   const bf16* kb = k + (long)kvh * nk * D;
   const bf16* vb = v + (long)kvh * nk * D;
 
-  // ---- K rows of this lane's key -> registers (B operand of S) ------------
+  // ---- K row of this lane's key -> registers (B operand of S); keys past nk
+  //      load key nk - 1 (computed, never stored) --------------------------
   bf16x8 kreg[DC];
   {
-    const bool ok = mykey < nk;
-    const bf16* kp = kb + (long)(ok ? mykey : 0) * D + 8 * g;
+    const bf16* kp = kb + (long)min(mykey, nk - 1) * D + 8 * g;
 #pragma unroll
-    for (int c = 0; c < DC; ++c)
-      kreg[c] = as_bf16x8(ok ? *reinterpret_cast<const u32x4*>(kp + 16 * c) : u32x4{0, 0, 0, 0});
+    for (int c = 0; c < DC; ++c) kreg[c] = as_bf16x8(*reinterpret_cast<const u32x4*>(kp + 16 * c));
   }
-  // ---- the block's V rows -> LDS (B operand of dP; keeps registers free) ----
-  for (int c = tid; c < BN * CPR; c += 256) {
-    const int row = c / CPR, col = (c % CPR) * 8;
-    const int key = n0 + row;
-    *reinterpret_cast<u32x4*>(&sm.vs[row][col]) =
-        key < nk ? *reinterpret_cast<const u32x4*>(vb + (long)key * D + col) : u32x4{0, 0, 0, 0};
+  // ---- the block's V rows -> LDS (SWZ_DUAL; keys past nk re-read key nk-1) ----
+  {
+    const auto vr = make_rsrc(vb, nk * D * 2);
+#pragma unroll
+    for (int i = 0; i < VCH; ++i) {
+      const int L = swz<SWZ_DUAL, D>(i * 256 + tid);  // the chunk this lane's slot holds
+      const int key = min(n0 + L / CPR, nk - 1);
+      dma16(vr, sm.v + i * 4096 + wave * 1024, key * D * 2 + (L % CPR) * 16, 0);
+    }
   }
 
-  // ---- query-block walk ------------------------------------------------------
+  // ---- query-block walk: (head, q-block) for every q head of the group ----
   const int qb_first = CAUSAL ? n0 / BM : 0;
-  const int n_qb = (nq + BM - 1) / BM;
-  const int iters_per_head = n_qb > qb_first ? n_qb - qb_first : 0;
-  const int n_iter = group * iters_per_head;
+  const int n_qb = nq_pad / BM;
+  const int per_head = n_qb > qb_first ? n_qb - qb_first : 0;
+  const int n_iter = group * per_head;
 
-  // Staging: a Q or dO tile is BM x CPR 16-byte chunks; each thread carries
-  // TCH chunks of both.
-  constexpr int TCH = BM * CPR / 256;
-  u32x4 qstage[TCH], dstage[TCH];
-  float st_lse = 0.0f, st_delta = 0.0f;
-  int cur_head = 0, cur_qb = qb_first;  // (head, q-block) of the tile being staged
-
-  auto load_tile = [&]() {
-    const long bh = (long)b * hq + (long)hk * group + cur_head;
-    const int qb0 = cur_qb * BM;
+  // Q / dO tiles: chunk P = i*256 + tid of a tile holds tile chunk swz(P);
+  // the swizzle repeats every 256 chunks.  Wave 0 also brings the rows'
+  // LSE / Delta (2*BM floats, one dword per lane).
+  const uint32_t src = swz<SWZ_DUAL, D>(tid) * 16;
+  auto load_tile = [&](int head, int qb, int buf) {
+    const long bh = (long)b * hq + (long)hk * group + head;
+    const int row0 = qb * BM;
+    const int bytes = (nq - row0) * D * 2;  // > 0: row0 < nq
+    const auto qr = make_rsrc(q + (bh * nq + row0) * D, bytes);
+    const auto dr = make_rsrc(dout + (bh * nq + row0) * D, bytes);
+    char* qdst = sm.q[buf] + wave * 1024;
+    char* ddst = sm.d[buf] + wave * 1024;
+    if (row0 + BM <= nq) {
 #pragma unroll
-    for (int i = 0; i < TCH; ++i) {
-      const int c = i * 256 + tid;
-      const int row = qb0 + c / CPR;
-      const long off = (bh * nq + row) * D + (c % CPR) * 8;
-      qstage[i] = row < nq ? *reinterpret_cast<const u32x4*>(q + off) : u32x4{0, 0, 0, 0};
-      dstage[i] = row < nq ? *reinterpret_cast<const u32x4*>(dout + off) : u32x4{0, 0, 0, 0};
+      for (int i = 0; i < TCH; ++i) {
+        dma16(qr, qdst + i * 4096, src + i * 4096, 0);
+        dma16(dr, ddst + i * 4096, src + i * 4096, 0);
+      }
+    } else {  // rows past nq re-read row nq - 1 (their LSE is +inf: P = 0)
+      const int lastrow = nq - 1 - row0;
+#pragma unroll
+      for (int i = 0; i < TCH; ++i) {
+        const int o = src + i * 4096;
+        const int oc = min(o / (2 * D), lastrow) * (2 * D) + o % (2 * D);
+        dma16(qr, qdst + i * 4096, oc, 0);
+        dma16(dr, ddst + i * 4096, oc, 0);
+      }
     }
-    if (tid >= 192 && tid < 192 + BM) {
-      int row = qb0 + (tid - 192);
-      st_lse = row < nq ? lse[bh * nq + row] * kLog2e : INFINITY;
-      st_delta = row < nq ? delta[bh * nq + row] : 0.0f;
-    }
-    if (++cur_qb == n_qb) {
-      cur_qb = qb_first;
-      ++cur_head;
+    if (wave == 0) {
+      const auto lr = make_rsrc(ld + (bh * nq_pad + row0) * 2, 2 * BM * 4);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(lr, (lds_void*)sm.ld[buf], 4, lane * 4, 0, 0, 0);
     }
   };
-  auto store_tile = [&](int buf) {
+
+  // ---- LDS read offsets (bytes) --------------------------------------------
+  // rows: lane reads row l32 (V: 32*wave + l32), column chunk 2c + g
+  int row_off[DC];
 #pragma unroll
-    for (int i = 0; i < TCH; ++i) {
-      const int c = i * 256 + tid;
-      *reinterpret_cast<u32x4*>(&sm.qs[buf][c / CPR][(c % CPR) * 8]) = qstage[i];
-      *reinterpret_cast<u32x4*>(&sm.dos[buf][c / CPR][(c % CPR) * 8]) = dstage[i];
+  for (int c = 0; c < DC; ++c) row_off[c] = swz<SWZ_DUAL, D>(l32 * CPR + 2 * c + g) * 16;
+  const char* vrows = sm.v + wave * 32 * D * 2;  // the swizzle repeats every 16 rows
+  // transposes (Q^T, dO^T): lane p of 16-lane group G reads row 8e + 4g + p/4
+  // (+16 hh) and 8 bytes at column 32t + 16(G%2) + 4(p%4)
+  int tr_off[DT][2];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int row = 8 * e + 4 * g + ((lane & 15) >> 2);
+      const int col = 32 * t + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+      tr_off[t][e] = swz<SWZ_DUAL, D>(row * CPR + col / 8) * 16 + (col % 8) * 2;
     }
-    if (tid >= 192 && tid < 192 + BM) {
-      sm.lse2[buf][tid - 192] = st_lse;
-      sm.delta[buf][tid - 192] = st_delta;
-    }
+  auto tr_read = [&](const char* tile, int hh, int t) {
+    const char* p = tile + hh * 16 * D * 2;
+    u32x2 a0 = lds_read_tr(p + tr_off[t][0]), a1 = lds_read_tr(p + tr_off[t][1]);
+    return as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
   };
 
   f32x16 dk_acc[DT], dv_acc[DT];
@@ -182,73 +201,121 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
   }
   const float sl2 = scale * kLog2e;
 
-  if (n_iter > 0) {
-    load_tile();
-    store_tile(0);
-  }
+  int head = 0, qb = qb_first;  // (head, q-block) of the tile in buffer `it & 1`
+  if (n_iter > 0) load_tile(0, qb_first, 0);
+  __builtin_amdgcn_s_waitcnt(0);  // V block and the first tile
   __syncthreads();
 
-  int qb = qb_first;  // q-block of the tile in LDS buffer `cur`
   for (int it = 0; it < n_iter; ++it) {
-    const int cur = it & 1;
+    const int buf = it & 1;
     const int qb0 = qb * BM;
-    if (++qb == n_qb) qb = qb_first;
-    if (it + 1 < n_iter) load_tile();
+    int nhead = head, nqb = qb + 1;
+    if (nqb == n_qb) {
+      nqb = qb_first;
+      ++nhead;
+    }
+    if (it + 1 < n_iter) load_tile(nhead, nqb, buf ^ 1);
+    const char* qt = sm.q[buf];
+    const char* dt = sm.d[buf];
+    const float* lt = sm.ld[buf];
 
-    const bool wave_active = !(CAUSAL && kw0 > qb0 + BM - 1) && kw0 < nk;
-    if (wave_active) {
-      const bool need_mask = (kw0 + 32 > nk) || (CAUSAL && kw0 + 31 > qb0);
-      // S = Q K^T and dP = dO V^T, C layout: lane = key (col), 16 query rows.
-      f32x16 s = f32x16{}, dp = f32x16{};
-      const bf16* qrow = &sm.qs[cur][l32][8 * g];
-      const bf16* drow = &sm.dos[cur][l32][8 * g];
-      const bf16* vrow = &sm.vs[32 * wave + l32][8 * g];
+    // ---- S = Q K^T (lane = key, 16 query rows); Q rows read KPF ahead ----
+    constexpr int KPF = 1;
+    f32x16 s = f32x16{}, dp = f32x16{};
+    {
+      u32x4 aq[DC];
+#pragma unroll
+      for (int c = 0; c < KPF; ++c) aq[c] = *reinterpret_cast<const u32x4*>(qt + row_off[c]);
 #pragma unroll
       for (int c = 0; c < DC; ++c) {
-        u32x4 aq = *reinterpret_cast<const u32x4*>(qrow + 16 * c);
-        s = mfma32(as_bf16x8(aq), kreg[c], s);
-        u32x4 ad = *reinterpret_cast<const u32x4*>(drow + 16 * c);
-        u32x4 bv = *reinterpret_cast<const u32x4*>(vrow + 16 * c);
-        dp = mfma32(as_bf16x8(ad), as_bf16x8(bv), dp);
+        if (c + KPF < DC) aq[c + KPF] = *reinterpret_cast<const u32x4*>(qt + row_off[c + KPF]);
+        s = mfma32(as_bf16x8(aq[c]), kreg[c], s);
       }
-      uint32_t pb[8], dsb[8];
+      sched_group(kDsRead, KPF);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r0 = 8 * j + 4 * g;  // first of this register group's 4 rows
-        f32x4 l4 = *reinterpret_cast<const f32x4*>(&sm.lse2[cur][r0]);
-        f32x4 d4 = *reinterpret_cast<const f32x4*>(&sm.delta[cur][r0]);
-        float p[4], ds[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float pv = fast_exp2(__builtin_fmaf(s[4 * j + i], sl2, -l4[i]));
-          if (need_mask) {
-            int qrow_i = qb0 + r0 + i;
-            if (mykey >= nk || (CAUSAL && mykey > qrow_i)) pv = 0.0f;
-          }
-          p[i] = pv;
-          ds[i] = pv * (dp[4 * j + i] - d4[i]);
-        }
-        pb[2 * j] = pack_bf16x2(p[0], p[1]);
-        pb[2 * j + 1] = pack_bf16x2(p[2], p[3]);
-        dsb[2 * j] = pack_bf16x2(ds[0], ds[1]);
-        dsb[2 * j + 1] = pack_bf16x2(ds[2], ds[3]);
-      }
-      // dV^T += dO^T P and dK^T += Q^T dS (keys = columns, queries summed).
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        bf16x8 bp = as_bf16x8(u32x4{pb[4 * hh], pb[4 * hh + 1], pb[4 * hh + 2], pb[4 * hh + 3]});
-        bf16x8 bs =
-            as_bf16x8(u32x4{dsb[4 * hh], dsb[4 * hh + 1], dsb[4 * hh + 2], dsb[4 * hh + 3]});
-#pragma unroll
-        for (int t = 0; t < DT; ++t) {
-          dv_acc[t] = mfma32(xt_operand<D + QPAD>(&sm.dos[cur][0][0], 16 * hh, 32 * t, lane), bp,
-                             dv_acc[t]);
-          dk_acc[t] = mfma32(xt_operand<D + QPAD>(&sm.qs[cur][0][0], 16 * hh, 32 * t, lane), bs,
-                             dk_acc[t]);
-        }
+      for (int c = 0; c < DC; ++c) {
+        if (c + KPF < DC) sched_group(kDsRead, 1);
+        sched_group(kMfma, 1);
       }
     }
-    if (it + 1 < n_iter) store_tile(cur ^ 1);
+    // ---- masking (boundary blocks only): scores -> -inf, so P = dS = 0 ----
+    if ((kw0 + 32 > nk) || (CAUSAL && kw0 + 31 > qb0)) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qrow = qb0 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (mykey >= nk || (CAUSAL && mykey > qrow)) s[r] = -INFINITY;
+      }
+    }
+    // ---- dP = dO V^T on the matrix cores, P = exp2(S log2e scale - LSE
+    //      log2e) on the VALU; issue order fenced ----
+    uint32_t pb[8], dsb[8];
+    {
+      constexpr int PPC = 8 / DC;  // P pairs per product
+      u32x4 ad[DC], av[DC];
+#pragma unroll
+      for (int c = 0; c < 1; ++c) {
+        ad[c] = *reinterpret_cast<const u32x4*>(dt + row_off[c]);
+        av[c] = *reinterpret_cast<const u32x4*>(vrows + row_off[c]);
+      }
+      f32x4 l4;
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        if (c + 1 < DC) {
+          ad[c + 1] = *reinterpret_cast<const u32x4*>(dt + row_off[c + 1]);
+          av[c + 1] = *reinterpret_cast<const u32x4*>(vrows + row_off[c + 1]);
+        }
+        dp = mfma32(as_bf16x8(ad[c]), as_bf16x8(av[c]), dp);
+#pragma unroll
+        for (int i = 0; i < PPC; ++i) {
+          const int r = 2 * (c * PPC + i);  // registers r, r+1: rows 8(r/4) + 4g + r%4
+          if ((r & 3) == 0) l4 = *reinterpret_cast<const f32x4*>(lt + 8 * (r >> 2) + 4 * g);
+          const float p0 = fast_exp2(__builtin_fmaf(s[r], sl2, -l4[r & 3]));
+          const float p1 = fast_exp2(__builtin_fmaf(s[r + 1], sl2, -l4[(r & 3) + 1]));
+          s[r] = p0;
+          s[r + 1] = p1;
+          pb[r >> 1] = pack_bf16x2(p0, p1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // ---- dV^T += dO^T P on the matrix cores, dS = P (dP - Delta) on the
+    //      VALU (hh = 0 pairs after the first product, hh = 1 after ...);
+    //      then dK^T += Q^T dS ----
+    {
+      constexpr int NJ = 2 * DT;   // products of dV^T
+      constexpr int PPJ = 8 / NJ;  // dS pairs per product
+      bf16x8 ta = tr_read(dt, 0, 0);
+      f32x4 d4;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int hh = j / DT, t = j % DT;
+        bf16x8 tn;
+        if (j + 1 < NJ) tn = tr_read(dt, (j + 1) / DT, (j + 1) % DT);
+        dv_acc[t] = mfma32(ta, as_bf16x8(u32x4{pb[4 * hh], pb[4 * hh + 1], pb[4 * hh + 2],
+                                                 pb[4 * hh + 3]}), dv_acc[t]);
+#pragma unroll
+        for (int i = 0; i < PPJ; ++i) {
+          const int r = 2 * (j * PPJ + i);
+          if ((r & 3) == 0) d4 = *reinterpret_cast<const f32x4*>(lt + BM + 8 * (r >> 2) + 4 * g);
+          dsb[r >> 1] = pack_bf16x2(s[r] * (dp[r] - d4[r & 3]), s[r + 1] * (dp[r + 1] - d4[(r & 3) + 1]));
+        }
+        if (j + 1 < NJ) ta = tn;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      ta = tr_read(qt, 0, 0);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int hh = j / DT, t = j % DT;
+        bf16x8 tn;
+        if (j + 1 < NJ) tn = tr_read(qt, (j + 1) / DT, (j + 1) % DT);
+        dk_acc[t] = mfma32(ta, as_bf16x8(u32x4{dsb[4 * hh], dsb[4 * hh + 1], dsb[4 * hh + 2],
+                                                  dsb[4 * hh + 3]}), dk_acc[t]);
+        if (j + 1 < NJ) ta = tn;
+      }
+    }
+    head = nhead;
+    qb = nqb;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of the next tile have landed
     __syncthreads();
   }
 
@@ -288,9 +355,8 @@ struct __attribute__((aligned(16))) DqSmem {
 template <int D, bool CAUSAL>
 __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ k,
                            const bf16* __restrict__ v, const bf16* __restrict__ dout,
-                           const float* __restrict__ lse, const float* __restrict__ delta,
-                           bf16* __restrict__ dq, int nq, int nk, float scale, int hq, int hkv,
-                           int num_m_blocks, int total_blocks) {
+                           const float* __restrict__ ld, bf16* __restrict__ dq, int nq, int nk,
+                           float scale, int hq, int hkv, int num_m_blocks, int total_blocks) {
   constexpr int DC = D / 16;
   constexpr int DT = D / 32;
   constexpr int CPR = D / 8;
@@ -329,8 +395,11 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
       doreg[c] = as_bf16x8(*reinterpret_cast<const u32x4*>(dp + 16 * c));
     }
   }
-  const float lse2 = qok ? lse[(long)bh * nq + qrow] * kLog2e : INFINITY;
-  const float dlt = qok ? delta[(long)bh * nq + qrow] : 0.0f;
+  // LSE * log2(e) and Delta of this row (rows past nq: +inf and 0)
+  const int nq_pad = (nq + BM - 1) / BM * BM;
+  const float* ldr = ld + ((long)bh * nq_pad + min(qrow, nq_pad - 1)) / BM * (2 * BM);
+  const float lse2 = qok ? ldr[qrow % BM] : INFINITY;
+  const float dlt = qok ? ldr[BM + qrow % BM] : 0.0f;
   const float sl2 = scale * kLog2e;
 
   int kend = nk;
@@ -520,36 +589,36 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
 
 #define TEENY_FA2_BWD_BF16_INST(D)                                                              \
   extern "C" __global__ __launch_bounds__(256) void teeny_fa2_bwd_pre_bf16_d##D(               \
-      const bf16* o, const bf16* dout, float* delta, long rows) {                               \
-    bwd_pre<D>(o, dout, delta, rows);                                                           \
+      const bf16* o, const bf16* dout, const float* lse, float* ld, int nq, long prows) {       \
+    bwd_pre<D>(o, dout, lse, ld, nq, prows);                                                    \
   }                                                                                             \
-  extern "C" __global__ __launch_bounds__(256) void teeny_fa2_bwd_dkdv_bf16_d##D##_c(          \
-      const bf16* q, const bf16* k, const bf16* v, const bf16* dout, const float* lse,          \
-      const float* delta, bf16* dk, bf16* dv, int nq, int nk, float scale, int hq, int hkv,     \
-      int nnb, int total) {                                                                     \
-    fa2_bwd_dkdv<D, true>(q, k, v, dout, lse, delta, dk, dv, nq, nk, scale, hq, hkv, nnb,      \
-                          total);                                                               \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
+  void teeny_fa2_bwd_dkdv_bf16_d##D##_c(const bf16* q, const bf16* k, const bf16* v,           \
+                                        const bf16* dout, const float* ld, bf16* dk, bf16* dv,  \
+                                        int nq, int nk, float scale, int hq, int hkv, int nnb,  \
+                                        int total) {                                            \
+    fa2_bwd_dkdv<D, true>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb, total);      \
   }                                                                                             \
-  extern "C" __global__ __launch_bounds__(256) void teeny_fa2_bwd_dkdv_bf16_d##D##_n(          \
-      const bf16* q, const bf16* k, const bf16* v, const bf16* dout, const float* lse,          \
-      const float* delta, bf16* dk, bf16* dv, int nq, int nk, float scale, int hq, int hkv,     \
-      int nnb, int total) {                                                                     \
-    fa2_bwd_dkdv<D, false>(q, k, v, dout, lse, delta, dk, dv, nq, nk, scale, hq, hkv, nnb,     \
-                           total);                                                              \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
+  void teeny_fa2_bwd_dkdv_bf16_d##D##_n(const bf16* q, const bf16* k, const bf16* v,           \
+                                        const bf16* dout, const float* ld, bf16* dk, bf16* dv,  \
+                                        int nq, int nk, float scale, int hq, int hkv, int nnb,  \
+                                        int total) {                                            \
+    fa2_bwd_dkdv<D, false>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb, total);     \
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
   void teeny_fa2_bwd_dq_bf16_d##D##_c(const bf16* q, const bf16* k, const bf16* v,             \
-                                      const bf16* dout, const float* lse, const float* delta,   \
-                                      bf16* dq, int nq, int nk, float scale, int hq, int hkv,   \
-                                      int nmb, int total) {                                     \
-    fa2_bwd_dq<D, true>(q, k, v, dout, lse, delta, dq, nq, nk, scale, hq, hkv, nmb, total);    \
+                                      const bf16* dout, const float* ld, bf16* dq, int nq,      \
+                                      int nk, float scale, int hq, int hkv, int nmb,            \
+                                      int total) {                                              \
+    fa2_bwd_dq<D, true>(q, k, v, dout, ld, dq, nq, nk, scale, hq, hkv, nmb, total);            \
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
   void teeny_fa2_bwd_dq_bf16_d##D##_n(const bf16* q, const bf16* k, const bf16* v,             \
-                                      const bf16* dout, const float* lse, const float* delta,   \
-                                      bf16* dq, int nq, int nk, float scale, int hq, int hkv,   \
-                                      int nmb, int total) {                                     \
-    fa2_bwd_dq<D, false>(q, k, v, dout, lse, delta, dq, nq, nk, scale, hq, hkv, nmb, total);   \
+                                      const bf16* dout, const float* ld, bf16* dq, int nq,      \
+                                      int nk, float scale, int hq, int hkv, int nmb,            \
+                                      int total) {                                              \
+    fa2_bwd_dq<D, false>(q, k, v, dout, ld, dq, nq, nk, scale, hq, hkv, nmb, total);           \
   }
 
 TEENY_FA2_BWD_BF16_INST(64)
