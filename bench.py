@@ -18,10 +18,13 @@ are resident in HBM before timing.  Prints one JSON line:
               forward (B4 S2048 d2048, Hq32/Hkv8, F8192, bf16), and the
               Llama-3-8B-shaped model (32 layers, d4096, Hq32/Hkv8, F14336,
               vocab 128256, random N(0, 0.02) bf16 weights): prefill of 16 x 512
-              tokens and 128 greedy KV-cached decode steps
+              tokens and 128 greedy KV-cached decode steps; and the board's
+              socket power and engine clock (amd-smi, median of samples)
+              while the step runs back to back for about two seconds: these
+              kernels hold the board at its power limit, which sets the clock
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--no-extra]
+                       [--no-extra] [--no-power]
 """
 from __future__ import annotations
 
@@ -56,6 +59,8 @@ def main() -> int:
                     help="heads of the workload the CPU baseline times")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the long-context GQA, Llama block and Llama-8B measurements")
+    ap.add_argument("--no-power", action="store_true",
+                    help="skip the power / clock sampling phase")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed steps, run one head transpose (a pure copy) of "
                          "Q's 256 MiB, the known-size reference for HBM byte counters")
@@ -163,6 +168,8 @@ def main() -> int:
         },
     }
 
+    if not args.no_power:
+        out["detail"]["power"] = sample_power(torch, step, seconds=2.0)
     if not args.no_extra:
         del q, k, v, do, o, lse, dq, dk, dv, ws
         torch.cuda.empty_cache()
@@ -270,6 +277,57 @@ def bench_llama_8b(torch):
             "decode_weight_gbs": round(wbytes / decode_ms / 1e6, 1),
             "decode_pct_hbm_peak": round(wbytes / decode_ms / 1e6 / PEAK_HBM_GBS, 4),
             "batch": Bq, "prompt": Sp, "new_tokens": n_new}
+
+
+def _smi_sample():
+    """(socket power W, mean engine clock MHz over the XCDs) from amd-smi, or None."""
+    import subprocess
+
+    try:
+        r = subprocess.run(["amd-smi", "metric", "-p", "-c", "--json"], capture_output=True,
+                           text=True, timeout=10)
+        d = json.loads(r.stdout)["gpu_data"]
+        g = d[0] if isinstance(d, list) else d
+        pw = float(g["power"]["socket_power"]["value"])
+        clks = [float(v["clk"]["value"]) for n, v in g["clock"].items() if n.startswith("gfx_")]
+        return pw, sum(clks) / len(clks)
+    except Exception:  # tool missing or output format differs: report nothing
+        return None
+
+
+def sample_power(torch, step, seconds: float):
+    """Runs `step` back to back for `seconds` while sampling amd-smi from a
+    thread; medians of the samples taken after the first half second."""
+    import statistics
+    import threading
+
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        t0 = time.perf_counter()
+        while not stop.is_set():
+            s = _smi_sample()
+            if s is not None and time.perf_counter() - t0 > 0.5:
+                samples.append(s)
+            time.sleep(0.1)
+
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    t0, n = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
+        n += 10
+    ms = (time.perf_counter() - t0) * 1e3 / n
+    stop.set()
+    th.join()
+    if not samples:
+        return None
+    return {"socket_power_w": statistics.median(p for p, _ in samples),
+            "engine_clock_mhz": round(statistics.median(c for _, c in samples)),
+            "max_engine_clock_mhz": 2400, "samples": len(samples),
+            "ms_per_step_while_sampling": round(ms, 4)}
 
 
 def traffic_from_profiles(kernel: str):
