@@ -25,6 +25,7 @@
 #define TEENY_HIP_H
 
 #include <stddef.h>
+#include <stdint.h>
 #include <hip/hip_runtime_api.h>
 
 #ifdef __cplusplus
@@ -225,6 +226,32 @@ int teeny_decode_attention(const void* q, const void* k_cache, const void* v_cac
                            int batch, int n_heads_q, int n_heads_kv, int n_keys, int cache_len,
                            int head_dim, float softmax_scale, int dtype, void* workspace,
                            size_t workspace_bytes, hipStream_t stream);
+
+/* Device-position variants for a decode step captured once in a HIP graph
+ * and replayed while the position advances (the reference has no KV cache
+ * and no graphs; these have no counterpart there).
+ * teeny_qkv_rope_split_dev: as teeny_qkv_rope_split with pos0 read from
+ *   device memory (*pos0) when the kernel runs; cache rows outside
+ *   [0, cache_len) are not written.
+ * teeny_decode_attention_dev: as teeny_decode_attention attending to the
+ *   first min(*n_past + 1, max_keys) cache rows, *n_past read when the kernel
+ *   runs; the grid and the workspace are sized for max_keys
+ *   (teeny_decode_attention_workspace_bytes(batch, n_heads_q, max_keys, D)). */
+int teeny_qkv_rope_split_dev(const void* qkv, void* q_out, void* k_cache, void* v_cache,
+                             int batch, int seq_len, const int32_t* pos0, int cache_len,
+                             int n_heads_q, int n_heads_kv, int head_dim, float ln_rope_base,
+                             int dtype, hipStream_t stream);
+int teeny_decode_attention_dev(const void* q, const void* k_cache, const void* v_cache, void* o,
+                               int batch, int n_heads_q, int n_heads_kv, const int32_t* n_past,
+                               int max_keys, int cache_len, int head_dim, float softmax_scale,
+                               int dtype, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream);
+
+/* Row argmax of x [rows, cols] -> out[rows] (int64): the first index of the
+ * maximum, NaN counting as the maximum (torch.argmax's convention); the
+ * reference's greedy choice (examples/llama_generate.rs:252-257). */
+int teeny_argmax_rows(const void* x, int64_t* out, int rows, int cols, int dtype,
+                      hipStream_t stream);
 
 #ifdef __cplusplus
 }

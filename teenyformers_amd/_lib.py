@@ -62,6 +62,10 @@ _SIGNATURES = {
     "teeny_qkv_rope_split": ([_p] * 4 + [_i] * 7 + [_f, _i, _p], _i),
     "teeny_decode_attention_workspace_bytes": ([_i] * 4, _sz),
     "teeny_decode_attention": ([_p] * 4 + [_i] * 6 + [_f, _i, _p, _sz, _p], _i),
+    "teeny_qkv_rope_split_dev": ([_p] * 4 + [_i, _i, _p] + [_i] * 4 + [_f, _i, _p], _i),
+    "teeny_decode_attention_dev": ([_p] * 4 + [_i] * 3 + [_p] + [_i] * 3
+                                   + [_f, _i, _p, _sz, _p], _i),
+    "teeny_argmax_rows": ([_p, _p, _i, _i, _i, _p], _i),
 }
 
 

@@ -32,7 +32,8 @@
   X(fa2_f32)             \
   X(fa2_fwd_bf16)        \
   X(fa2_bwd_bf16)        \
-  X(llama)
+  X(llama)               \
+  X(decode_bf16)
 
 #define TEENY_CO_DECL(n) \
   extern "C" const unsigned char teeny_co_##n[]; \
@@ -593,9 +594,10 @@ int teeny_swiglu_bwd(const void* grad, const void* z, void* dz, int M, int d_ff,
   return swiglu_impl(true, grad, z, dz, M, d_ff, dtype, stream);
 }
 
-int teeny_qkv_rope_split(const void* qkv, void* q_out, void* k_cache, void* v_cache, int batch,
-                         int seq_len, int pos0, int cache_len, int n_heads_q, int n_heads_kv,
-                         int head_dim, float ln_rope_base, int dtype, hipStream_t stream) {
+static int qkv_rope_split_impl(const void* qkv, void* q_out, void* k_cache, void* v_cache,
+                               int batch, int seq_len, const int32_t* pos_dev, int pos0,
+                               int cache_len, int n_heads_q, int n_heads_kv, int head_dim,
+                               float ln_rope_base, int dtype, hipStream_t stream) {
   if (!qkv || !q_out || !k_cache || !v_cache) return TEENY_ERR_NULL_POINTER;
   if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
   if (batch <= 0 || seq_len <= 0 || pos0 < 0 || n_heads_q <= 0 || n_heads_kv <= 0 ||
@@ -611,25 +613,56 @@ int teeny_qkv_rope_split(const void* qkv, void* q_out, void* k_cache, void* v_ca
   if (gy > 65535) return TEENY_ERR_INVALID_SHAPE;
   char name[48];
   snprintf(name, sizeof name, "teeny_qkv_rope_split_%s", dtype_tag(dtype));
-  void* args[] = {&qkv, &q_out, &k_cache, &v_cache, &seq_len, &pos0, &cache_len,
-                  &n_heads_q, &n_heads_kv, &head_dim, &ln_rope_base};
+  void* args[] = {&qkv,      &q_out,     &k_cache,   &v_cache,    &seq_len,   &pos_dev,
+                  &pos0,     &cache_len, &n_heads_q, &n_heads_kv, &head_dim,  &ln_rope_base};
   unsigned shmem = 16u * (unsigned)(head_dim / 2) * 8u;
   return launch(name, dim3((seq_len + 15) / 16, (unsigned)gy), dim3(256), shmem, stream, args);
 }
 
-static int decode_chunks(int n_keys) { return (n_keys + 255) / 256; }
+int teeny_qkv_rope_split(const void* qkv, void* q_out, void* k_cache, void* v_cache, int batch,
+                         int seq_len, int pos0, int cache_len, int n_heads_q, int n_heads_kv,
+                         int head_dim, float ln_rope_base, int dtype, hipStream_t stream) {
+  return qkv_rope_split_impl(qkv, q_out, k_cache, v_cache, batch, seq_len, nullptr, pos0,
+                             cache_len, n_heads_q, n_heads_kv, head_dim, ln_rope_base, dtype,
+                             stream);
+}
+
+int teeny_qkv_rope_split_dev(const void* qkv, void* q_out, void* k_cache, void* v_cache,
+                             int batch, int seq_len, const int32_t* pos0, int cache_len,
+                             int n_heads_q, int n_heads_kv, int head_dim, float ln_rope_base,
+                             int dtype, hipStream_t stream) {
+  if (!pos0) return TEENY_ERR_NULL_POINTER;
+  return qkv_rope_split_impl(qkv, q_out, k_cache, v_cache, batch, seq_len, pos0, 0, cache_len,
+                             n_heads_q, n_heads_kv, head_dim, ln_rope_base, dtype, stream);
+}
+
+static int decode_chunks(int n_keys) { return (n_keys + 255) / 256; }  // fp32 kernel
+
+// bf16 matrix-core kernel: keys per wavefront chosen so that one step runs
+// about 2048 wavefronts (a multiple of the 32-key tile, 64 .. 1024).
+static int decode_keys_per_split(int n_keys, int batch, int n_heads_kv) {
+  long per = ((long)n_keys * batch * n_heads_kv + 2047) / 2048;
+  per = (per + 31) / 32 * 32;
+  if (per < 64) per = 64;
+  if (per > 1024) per = 1024;
+  return (int)per;
+}
 
 size_t teeny_decode_attention_workspace_bytes(int batch, int n_heads_q, int n_keys,
                                               int head_dim) {
   if (batch <= 0 || n_heads_q <= 0 || n_keys <= 0 || head_dim <= 0) return 0;
-  size_t rows = (size_t)batch * n_heads_q * decode_chunks(n_keys);
+  // the finest split either kernel uses: 64 keys
+  size_t rows = (size_t)batch * n_heads_q * ((n_keys + 63) / 64);
   return 2 * align256(rows * sizeof(float)) + align256(rows * head_dim * sizeof(float));
 }
 
-int teeny_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* o,
-                           int batch, int n_heads_q, int n_heads_kv, int n_keys, int cache_len,
-                           int head_dim, float softmax_scale, int dtype, void* workspace,
-                           size_t workspace_bytes, hipStream_t stream) {
+// n_keys: the keys attended (host value), or with n_past the grid's capacity
+// and the kernel attends *n_past + 1 of them.
+static int decode_attention_impl(const void* q, const void* k_cache, const void* v_cache,
+                                 void* o, int batch, int n_heads_q, int n_heads_kv,
+                                 const int32_t* n_past, int n_keys, int cache_len, int head_dim,
+                                 float softmax_scale, int dtype, void* workspace,
+                                 size_t workspace_bytes, hipStream_t stream) {
   if (!q || !k_cache || !v_cache || !o) return TEENY_ERR_NULL_POINTER;
   if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
   if (batch <= 0 || n_heads_q <= 0 || n_heads_kv <= 0 || n_heads_q % n_heads_kv != 0 ||
@@ -643,20 +676,66 @@ int teeny_decode_attention(const void* q, const void* k_cache, const void* v_cac
   if (!workspace ||
       workspace_bytes < teeny_decode_attention_workspace_bytes(batch, n_heads_q, n_keys, head_dim))
     return TEENY_ERR_WORKSPACE;
-  int n_chunks = decode_chunks(n_keys);
+  // the matrix-core kernel addresses one (b, kv head) cache slab with 32-bit
+  // byte offsets
+  const bool mfma = dtype == TEENY_BF16 && (head_dim == 64 || head_dim == 128) &&
+                    (long)cache_len * head_dim * 2 < (1L << 31);
+  const int per = mfma ? decode_keys_per_split(n_keys, batch, n_heads_kv) : 256;
+  int n_chunks = mfma ? (n_keys + per - 1) / per : decode_chunks(n_keys);
   size_t rows = (size_t)batch * n_heads_q * n_chunks;
   float* pm = (float*)workspace;
   float* pl = (float*)((char*)workspace + align256(rows * sizeof(float)));
   float* po = (float*)((char*)workspace + 2 * align256(rows * sizeof(float)));
   char name[48];
-  snprintf(name, sizeof name, "teeny_decode_attn_partial_%s", dtype_tag(dtype));
-  void* a0[] = {&q, &k_cache, &v_cache, &pm, &pl, &po, &n_heads_q, &n_heads_kv,
-                &n_keys, &cache_len, &head_dim, &softmax_scale};
-  int rc = launch(name, dim3(n_chunks, batch * n_heads_kv), dim3(256), 0, stream, a0);
+  int rc;
+  if (mfma) {
+    snprintf(name, sizeof name, "teeny_decode_mfma_bf16_d%d", head_dim);
+    int per_split = per;
+    void* a0[] = {&q,  &k_cache, &v_cache, &pm,        &pl,        &po,           &n_heads_q,
+                  &n_heads_kv, &n_past,  &n_keys,   &cache_len, &per_split, &softmax_scale};
+    rc = launch(name, dim3(n_chunks, batch * n_heads_kv), dim3(64), 0, stream, a0);
+  } else {
+    snprintf(name, sizeof name, "teeny_decode_attn_partial_%s", dtype_tag(dtype));
+    void* a0[] = {&q,      &k_cache, &v_cache,   &pm,       &pl,           &po, &n_heads_q,
+                  &n_heads_kv, &n_past, &n_keys, &cache_len, &head_dim, &softmax_scale};
+    rc = launch(name, dim3(n_chunks, batch * n_heads_kv), dim3(256), 0, stream, a0);
+  }
   if (rc) return rc;
   snprintf(name, sizeof name, "teeny_decode_attn_combine_%s", dtype_tag(dtype));
   void* a1[] = {&pm, &pl, &po, &o, &n_chunks, &head_dim};
   return launch(name, dim3(batch * n_heads_q), dim3(head_dim), 0, stream, a1);
+}
+
+int teeny_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* o,
+                           int batch, int n_heads_q, int n_heads_kv, int n_keys, int cache_len,
+                           int head_dim, float softmax_scale, int dtype, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
+  return decode_attention_impl(q, k_cache, v_cache, o, batch, n_heads_q, n_heads_kv, nullptr,
+                               n_keys, cache_len, head_dim, softmax_scale, dtype, workspace,
+                               workspace_bytes, stream);
+}
+
+int teeny_decode_attention_dev(const void* q, const void* k_cache, const void* v_cache, void* o,
+                               int batch, int n_heads_q, int n_heads_kv, const int32_t* n_past,
+                               int max_keys, int cache_len, int head_dim, float softmax_scale,
+                               int dtype, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream) {
+  if (!n_past) return TEENY_ERR_NULL_POINTER;
+  return decode_attention_impl(q, k_cache, v_cache, o, batch, n_heads_q, n_heads_kv, n_past,
+                               max_keys, cache_len, head_dim, softmax_scale, dtype, workspace,
+                               workspace_bytes, stream);
+}
+
+int teeny_argmax_rows(const void* x, int64_t* out, int rows, int cols, int dtype,
+                      hipStream_t stream) {
+  if (!x || !out) return TEENY_ERR_NULL_POINTER;
+  if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
+  if (rows <= 0 || cols <= 0 || (long)rows * cols >= kMaxElems * 2)
+    return TEENY_ERR_INVALID_SHAPE;
+  char name[48];
+  snprintf(name, sizeof name, "teeny_argmax_rows_%s", dtype_tag(dtype));
+  void* args[] = {&x, &out, &cols};
+  return launch(name, dim3(rows), dim3(1024), 0, stream, args);
 }
 
 int teeny_token_embed_fwd(const void* ids, const void* weight, void* out, int seq_len,

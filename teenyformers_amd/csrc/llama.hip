@@ -7,6 +7,9 @@
 //   (src/layers/attention.rs:97-123; transpose_heads.rs:49-71, rope.rs:57-97)
 //   with the same arithmetic: interleaved pairs, theta = fp32(pos) *
 //   fp32(exp_f64(fp32(k) * (-2 ln_base / D))), position = absolute position.
+//   pos0 may instead be read from device memory (a captured decode step whose
+//   position advances between replays); rows whose position falls outside
+//   the cache are then not written to it.
 //
 // teeny_decode_attn_*: one new query row per (b, q head) against the first
 //   n_keys cached keys (flash-decoding: split-K partials over 256-key chunks,
@@ -24,9 +27,10 @@ constexpr int kRows = 16;   // head rows (of Hq + 2 Hkv) per workgroup
 template <typename T>
 __device__ void qkv_rope_split(const T* __restrict__ qkv, T* __restrict__ q_out,
                                T* __restrict__ k_cache, T* __restrict__ v_cache, int seq,
-                               int pos0, int cache_len, int hq, int hkv, int head_dim,
-                               float ln_base) {
+                               const int* __restrict__ pos_dev, int pos0, int cache_len, int hq,
+                               int hkv, int head_dim, float ln_base) {
   extern __shared__ float2 cs_tab[];  // [kPos][head_dim / 2]
+  if (pos_dev) pos0 += *pos_dev;
   const int half = head_dim / 2;
   const int s0 = blockIdx.x * kPos;
   const int htot = hq + 2 * hkv;
@@ -36,6 +40,7 @@ __device__ void qkv_rope_split(const T* __restrict__ qkv, T* __restrict__ q_out,
   const float c = (-2.0f * ln_base) / (float)head_dim;
   for (int i = threadIdx.x; i < kPos * half; i += kThreads) {
     int p = i / half, k = i - p * half;
+    if (s0 + p >= seq) break;  // i grows with p: no later entry is needed either
     float inv = (float)exp((double)((float)k * c));
     float theta = (float)(pos0 + s0 + p) * inv;
     float sn, cn;
@@ -53,6 +58,7 @@ __device__ void qkv_rope_split(const T* __restrict__ qkv, T* __restrict__ q_out,
     int hh = h0 + r / kPos;
     int s = s0 + p;
     if (s >= seq || hh >= htot) continue;
+    if (hh >= hq && (pos0 + s < 0 || pos0 + s >= cache_len)) continue;  // outside the cache
     float in[VN];
     Vec16<T>::load(qkv + ((long)b * seq + s) * htot * head_dim + (long)hh * head_dim + v * VN, in);
     T* dst;
@@ -88,11 +94,15 @@ constexpr int kMaxD = 128;
 
 // grid (n_chunks, B * Hkv); q [B, Hq, D], caches [B, Hkv, cache_len, D].
 // Partials: m, l [B*Hq, n_chunks]; o [B*Hq, n_chunks, D] (unnormalised).
+// n_keys = n_keys_imm, or *n_past + 1 (the cached keys plus the new one)
+// when n_past is given, clamped to the keys the grid covers and the cache.
 template <typename T>
 __device__ void decode_partial(const T* __restrict__ q, const T* __restrict__ kc,
                                const T* __restrict__ vc, float* __restrict__ pm,
                                float* __restrict__ pl, float* __restrict__ po, int hq, int hkv,
-                               int n_keys, int cache_len, int head_dim, float scale) {
+                               const int* __restrict__ n_past, int n_keys, int cache_len,
+                               int head_dim, float scale) {
+  if (n_past) n_keys = min(min(*n_past + 1, (int)gridDim.x * kChunk), cache_len);
   __shared__ float qs[kMaxGroup][kMaxD];
   __shared__ float ps[kMaxGroup][kChunk];
   __shared__ float red[kMaxGroup][kThreads / 64];
@@ -231,23 +241,89 @@ __device__ void decode_combine(const float* __restrict__ pm, const float* __rest
   o[row * head_dim + d] = (T)(acc / l);
 }
 
+// Row argmax: one workgroup of 1024 threads per row, 16-byte loads; the
+// first index of the maximum (NaN counts as the maximum), as torch.argmax.
+constexpr int kArgThreads = 1024;
+template <typename T>
+__device__ void argmax_rows(const T* __restrict__ x, long long* __restrict__ out, int cols) {
+  __shared__ float bv[kArgThreads / 64];
+  __shared__ int bi[kArgThreads / 64];
+  const T* row = x + (long)blockIdx.x * cols;
+  float v = -INFINITY;
+  int idx = 0x7fffffff;
+  // a beats b: larger, or NaN over a number, or equal with the smaller index
+  auto better = [](float a, int ia, float b, int ib) {
+    const bool an = a != a, bn = b != b;
+    if (an || bn) return an && (!bn || ia < ib);
+    return a > b || (a == b && ia < ib);
+  };
+  constexpr int VN = Vec16<T>::N;
+  if (cols % VN == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
+    for (int c = threadIdx.x * VN; c < cols; c += kArgThreads * VN) {
+      float a[VN];
+      Vec16<T>::load(row + c, a);
+#pragma unroll
+      for (int j = 0; j < VN; ++j)
+        if (better(a[j], c + j, v, idx)) {
+          v = a[j];
+          idx = c + j;
+        }
+    }
+  } else {
+    for (int c = threadIdx.x; c < cols; c += kArgThreads) {
+      const float a = (float)row[c];
+      if (better(a, c, v, idx)) {
+        v = a;
+        idx = c;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(v, off, 64);
+    const int oi = __shfl_xor(idx, off, 64);
+    if (better(ov, oi, v, idx)) {
+      v = ov;
+      idx = oi;
+    }
+  }
+  if ((threadIdx.x & 63) == 0) {
+    bv[threadIdx.x >> 6] = v;
+    bi[threadIdx.x >> 6] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kArgThreads / 64; ++w)
+      if (better(bv[w], bi[w], v, idx)) {
+        v = bv[w];
+        idx = bi[w];
+      }
+    out[blockIdx.x] = idx;
+  }
+}
+
 }  // namespace
 
 #define TEENY_LLAMA_INST(TN, T)                                                                 \
   extern "C" __global__ __launch_bounds__(256) void teeny_qkv_rope_split_##TN(                 \
-      const T* qkv, T* q_out, T* k_cache, T* v_cache, int seq, int pos0, int cache_len, int hq, \
-      int hkv, int head_dim, float ln_base) {                                                   \
-    qkv_rope_split<T>(qkv, q_out, k_cache, v_cache, seq, pos0, cache_len, hq, hkv, head_dim,    \
-                      ln_base);                                                                 \
+      const T* qkv, T* q_out, T* k_cache, T* v_cache, int seq, const int* pos_dev, int pos0,    \
+      int cache_len, int hq, int hkv, int head_dim, float ln_base) {                            \
+    qkv_rope_split<T>(qkv, q_out, k_cache, v_cache, seq, pos_dev, pos0, cache_len, hq, hkv,     \
+                      head_dim, ln_base);                                                       \
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(256) void teeny_decode_attn_partial_##TN(            \
       const T* q, const T* kc, const T* vc, float* pm, float* pl, float* po, int hq, int hkv,   \
-      int n_keys, int cache_len, int head_dim, float scale) {                                   \
-    decode_partial<T>(q, kc, vc, pm, pl, po, hq, hkv, n_keys, cache_len, head_dim, scale);      \
+      const int* n_past, int n_keys, int cache_len, int head_dim, float scale) {                \
+    decode_partial<T>(q, kc, vc, pm, pl, po, hq, hkv, n_past, n_keys, cache_len, head_dim,      \
+                      scale);                                                                   \
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(256) void teeny_decode_attn_combine_##TN(            \
       const float* pm, const float* pl, const float* po, T* o, int n_chunks, int head_dim) {    \
     decode_combine<T>(pm, pl, po, o, n_chunks, head_dim);                                       \
+  }                                                                                             \
+  extern "C" __global__ __launch_bounds__(1024) void teeny_argmax_rows_##TN(                   \
+      const T* x, long long* out, int cols) {                                                   \
+    argmax_rows<T>(x, out, cols);                                                               \
   }
 
 TEENY_LLAMA_INST(f32, float)

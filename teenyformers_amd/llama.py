@@ -123,8 +123,9 @@ class Llama:
         self.decode_ws = None
 
     # -- one block (src/layers/llama_block.rs:55-65) -------------------------
-    def _attention(self, i: int, n1: torch.Tensor, cache: KVCache, pos0: int) -> torch.Tensor:
-        """src/layers/attention.rs:83-148 with GQA and a KV cache."""
+    def _attention(self, i: int, n1: torch.Tensor, cache: KVCache, pos0) -> torch.Tensor:
+        """src/layers/attention.rs:83-148 with GQA and a KV cache.  pos0: an int,
+        or (one-token decode in a captured graph) an int32 device tensor."""
         cfg, w = self.cfg, self.w
         B, S, d = n1.shape
         Hq, Hkv, D = cfg.n_heads, cfg.n_kv_heads(), cfg.head_dim()
@@ -133,13 +134,16 @@ class Llama:
         q = torch.empty((B, Hq, S, D), dtype=n1.dtype, device=n1.device)
         ops.qkv_rope_split(qkv, q, cache.k[i], cache.v[i], pos0, Hq, Hkv, cfg.rope_base)
         scale = cfg.softmax_scale()
-        if S == 1 and pos0 > 0:  # decode: the new row sees every cached key
-            if self.decode_ws is None:
-                self.decode_ws = torch.empty(
-                    ops._lib.lib().teeny_decode_attention_workspace_bytes(
-                        B, Hq, cache.capacity, D), dtype=torch.uint8, device=n1.device)
+        if isinstance(pos0, torch.Tensor):  # graph decode: the position is on the device
+            if S != 1:
+                raise ValueError("a device position is for one-token decode steps")
+            o = ops.decode_attention(q.view(B, Hq, D), cache.k[i], cache.v[i], cache.capacity,
+                                     scale, workspace=self._decode_ws(B, cache, n1.device),
+                                     n_past=pos0).view(B, Hq, 1, D)
+        elif S == 1 and pos0 > 0:  # decode: the new row sees every cached key
             o = ops.decode_attention(q.view(B, Hq, D), cache.k[i], cache.v[i], pos0 + 1, scale,
-                                     workspace=self.decode_ws).view(B, Hq, 1, D)
+                                     workspace=self._decode_ws(B, cache, n1.device)
+                                     ).view(B, Hq, 1, D)
         else:
             if pos0 != 0:
                 raise ValueError("prefill must start at position 0")
@@ -147,15 +151,24 @@ class Llama:
             o, _ = ops.flash_attn2_fwd(q, cache.k[i], cache.v[i], scale, causal=True)
         return F.linear(ops.merge_heads(o), w[p + "o_proj.weight"])
 
+    def _decode_ws(self, B: int, cache: KVCache, device) -> torch.Tensor:
+        """Split-K workspace for decode attention over the whole cache."""
+        need = ops._lib.lib().teeny_decode_attention_workspace_bytes(
+            B, self.cfg.n_heads, cache.capacity, self.cfg.head_dim())
+        if self.decode_ws is None or self.decode_ws.numel() < need:
+            self.decode_ws = torch.empty(need, dtype=torch.uint8, device=device)
+        return self.decode_ws
+
     def _ffn(self, i: int, n2: torch.Tensor) -> torch.Tensor:
         """src/layers/ffn.rs:47-56."""
         p = f"model.layers.{i}.mlp."
         z = F.linear(n2, self.w[p + "gate_up_proj.weight"])
         return F.linear(ops.swiglu(z), self.w[p + "down_proj.weight"])
 
-    def hidden(self, ids: torch.Tensor, cache: KVCache, pos0: int) -> torch.Tensor:
+    def hidden(self, ids: torch.Tensor, cache: KVCache, pos0) -> torch.Tensor:
         """Final-norm hidden states [B, S, d] for ids [B, S] at positions pos0..,
-        appending the new keys/values to `cache`."""
+        appending the new keys/values to `cache` (pos0 may be an int32 device
+        tensor for one-token steps; cache.length is then left to the caller)."""
         cfg, w = self.cfg, self.w
         x = ops.token_embed(ids.to(torch.int32).contiguous(), w["model.embed_tokens.weight"])
         eps = cfg.eps
@@ -170,7 +183,8 @@ class Llama:
             n2, x, _ = ops.fused_add_rmsnorm(a, x, w[p + "post_attention_layernorm.weight"], eps)
             delta = self._ffn(i, n2)
         y, _, _ = ops.fused_add_rmsnorm(delta, x, w["model.norm.weight"], eps)
-        cache.length = pos0 + ids.shape[1]
+        if not isinstance(pos0, torch.Tensor):
+            cache.length = pos0 + ids.shape[1]
         return y
 
     def logits(self, h: torch.Tensor) -> torch.Tensor:
@@ -206,6 +220,20 @@ class Llama:
             if len(out) == n_new:
                 break
             logits = self.decode_step(cache, nxt)
+        return torch.cat(out, dim=1)
+
+    def generate_graph(self, prompt: torch.Tensor, n_new: int) -> torch.Tensor:
+        """generate(), with the decode step captured once in a HIP graph and
+        replayed (same ids; no per-step launch overhead)."""
+        cache, logits = self.prefill(prompt, prompt.shape[1] + n_new)
+        first = ops.argmax_rows(logits).view(-1, 1)
+        if n_new == 1:
+            return first
+        dg = DecodeGraph(self, cache, first)  # runs decode step 1 while capturing
+        out = [first, dg.ids.clone()]
+        while len(out) < n_new:
+            dg.replay()
+            out.append(dg.ids.clone())
         return torch.cat(out, dim=1)
 
     def generate_recompute(self, prompt: torch.Tensor, n_new: int) -> torch.Tensor:
@@ -246,3 +274,43 @@ def prefill_flops(cfg: LlamaConfig, batch: int, seq: int, last_logits_only: bool
     f += cfg.n_layers * batch * 4.0 * seq * seq / 2 * Hq * D
     f += 2.0 * d * cfg.vocab_size * (batch if last_logits_only else tokens)
     return f
+
+
+class DecodeGraph:
+    """One greedy decode step (embed, every block with the KV cache, final
+    norm, tied lm_head on the last position, argmax) captured in a HIP graph.
+    The step reads its ids from `ids` [B, 1] (int64) and the cache length
+    from `pos` (int32, device); replay() writes the next ids into `ids`,
+    appends one cache row and advances `pos`.  The constructor runs the first
+    step eagerly on a side stream (the capture needs its libraries warmed up)
+    and then captures it, so after construction `ids` holds step 1's output.
+    Positions past the cache capacity are not written (the kernels check)."""
+
+    def __init__(self, model: Llama, cache: KVCache, ids: torch.Tensor):
+        self.model, self.cache = model, cache
+        self.ids = ids.to(torch.int64).clone()
+        self.pos = torch.full((1,), cache.length, dtype=torch.int32, device=ids.device)
+        model._decode_ws(ids.shape[0], cache, ids.device)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self._step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        cache.length += 1
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+
+    def _step(self):
+        m = self.model
+        h = m.hidden(self.ids, self.cache, self.pos)
+        nxt = ops.argmax_rows(m.logits(h[:, -1]))
+        self.ids.copy_(nxt.view(-1, 1))
+        self.pos.add_(1)
+
+    def replay(self):
+        if self.cache.length >= self.cache.capacity:
+            raise RuntimeError("KV cache is full")
+        self.graph.replay()
+        self.cache.length += 1

@@ -334,20 +334,31 @@ def _ln(rope_base: float) -> float:
     return float(torch.tensor(rope_base, dtype=torch.float32).log().item())
 
 
-def qkv_rope_split(qkv, q_out, k_cache, v_cache, pos0: int, n_heads_q: int, n_heads_kv: int,
+def qkv_rope_split(qkv, q_out, k_cache, v_cache, pos0, n_heads_q: int, n_heads_kv: int,
                    rope_base: float):
     """qkv [B, S, (Hq+2Hkv)*D] -> q_out [B, Hq, S, D] (RoPE) and K (RoPE) / V
-    written to caches [B, Hkv, L, D] at rows pos0 .. pos0+S-1."""
+    written to caches [B, Hkv, L, D] at rows pos0 .. pos0+S-1.  pos0: an int,
+    or a one-element int32 device tensor read when the kernel runs (for
+    captured graphs)."""
     _dev(qkv, q_out, k_cache, v_cache)
     B, S, _ = qkv.shape
     D = q_out.shape[-1]
+    if isinstance(pos0, torch.Tensor):
+        if pos0.dtype != torch.int32 or not pos0.is_cuda:
+            raise TypeError("a device position must be an int32 CUDA tensor")
+        call("teeny_qkv_rope_split_dev", _p(qkv), _p(q_out), _p(k_cache), _p(v_cache), B, S,
+             _p(pos0), k_cache.shape[2], n_heads_q, n_heads_kv, D, _ln(rope_base), _code(qkv),
+             _stream())
+        return
     call("teeny_qkv_rope_split", _p(qkv), _p(q_out), _p(k_cache), _p(v_cache), B, S, pos0,
          k_cache.shape[2], n_heads_q, n_heads_kv, D, _ln(rope_base), _code(qkv), _stream())
 
 
 def decode_attention(q, k_cache, v_cache, n_keys: int, softmax_scale: float | None = None,
-                     out=None, workspace=None):
-    """q [B, Hq, D] (one new row per head) over cache rows 0 .. n_keys-1."""
+                     out=None, workspace=None, n_past=None):
+    """q [B, Hq, D] (one new row per head) over cache rows 0 .. n_keys-1; with
+    n_past (a one-element int32 device tensor, read when the kernel runs) over
+    rows 0 .. min(n_past + 1, n_keys) - 1."""
     _dev(q, k_cache, v_cache)
     B, Hq, D = q.shape
     Hkv, L = k_cache.shape[1], k_cache.shape[2]
@@ -356,6 +367,26 @@ def decode_attention(q, k_cache, v_cache, n_keys: int, softmax_scale: float | No
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     out = torch.empty_like(q) if out is None else out
+    if n_past is not None:
+        if n_past.dtype != torch.int32 or not n_past.is_cuda:
+            raise TypeError("n_past must be an int32 CUDA tensor")
+        call("teeny_decode_attention_dev", _p(q), _p(k_cache), _p(v_cache), _p(out), B, Hq, Hkv,
+             _p(n_past), n_keys, L, D, scale, _code(q), _p(workspace), workspace.numel(),
+             _stream())
+        return out
     call("teeny_decode_attention", _p(q), _p(k_cache), _p(v_cache), _p(out), B, Hq, Hkv,
          n_keys, L, D, scale, _code(q), _p(workspace), workspace.numel(), _stream())
+    return out
+
+
+def argmax_rows(x, out=None):
+    """x [rows, cols] -> int64 [rows]: first index of each row's maximum
+    (NaN counts as the maximum), like torch.argmax(x, dim=-1)."""
+    _dev(x)
+    x2 = x.reshape(-1, x.shape[-1])
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    rows, cols = x2.shape
+    out = torch.empty(rows, dtype=torch.int64, device=x.device) if out is None else out
+    call("teeny_argmax_rows", _p(x2), _p(out), rows, cols, _code(x2), _stream())
     return out

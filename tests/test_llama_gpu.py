@@ -53,9 +53,14 @@ def test_qkv_rope_split(cuda, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("n_keys,D,Hq,Hkv", [(1, 64, 4, 4), (300, 128, 32, 8), (700, 64, 8, 1)])
-def test_decode_attention(cuda, dtype, n_keys, D, Hq, Hkv):
-    B, L = 3, 768
+@pytest.mark.parametrize("n_keys,L,D,Hq,Hkv", [
+    (1, 768, 64, 4, 4), (300, 768, 128, 32, 8), (700, 768, 64, 8, 1),
+    # cache length off the 32-key tile: the last tile re-reads the last row
+    (757, 757, 128, 16, 1),
+    # many key splits, the last holding one key
+    (2049, 4100, 128, 8, 8), (5000, 5000, 64, 32, 2)])
+def test_decode_attention(cuda, dtype, n_keys, L, D, Hq, Hkv):
+    B = 3
     g = torch.Generator(device="cuda").manual_seed(4)
     q = torch.randn((B, Hq, D), generator=g, device="cuda").to(dtype)
     kc = torch.randn((B, Hkv, L, D), generator=g, device="cuda").to(dtype)
@@ -153,3 +158,59 @@ def test_generate_cached_equals_recompute(cuda, n_kv):
     full = model.forward(prompt)
     _, last = model.prefill(prompt, 32)
     assert torch.allclose(full[:, -1], last, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_argmax_rows(cuda, dtype):
+    """First index of the row maximum, NaN counting as the maximum (torch.argmax)."""
+    g = torch.Generator(device="cuda").manual_seed(21)
+    x = torch.randn((16, 128256), generator=g, device="cuda").to(dtype)
+    x[3, 7] = x[3, 90000] = 1e4  # tie: the first index wins
+    x[5, :] = 0.0                # all equal: index 0
+    x[9, 123] = float("nan")     # NaN is the maximum
+    got = ops.argmax_rows(x)
+    assert torch.equal(got, torch.argmax(x, dim=-1))
+    assert got[3] == 7 and got[5] == 0 and got[9] == 123
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_device_position_variants(cuda, dtype):
+    """qkv_rope_split / decode_attention with the position in device memory
+    equal the host-position calls; a position past the cache writes nothing."""
+    B, Hq, Hkv, D, L, base = 2, 8, 2, 64, 300, 5e5
+    g = torch.Generator(device="cuda").manual_seed(22)
+    qkv = torch.randn((B, 1, (Hq + 2 * Hkv) * D), generator=g, device="cuda").to(dtype)
+    kc0 = torch.randn((B, Hkv, L, D), generator=g, device="cuda").to(dtype)
+    vc0 = torch.randn((B, Hkv, L, D), generator=g, device="cuda").to(dtype)
+    for pos in (0, 17, 299):
+        q_h, q_d = (torch.empty((B, Hq, 1, D), dtype=dtype, device="cuda") for _ in range(2))
+        kh, vh, kd, vd = kc0.clone(), vc0.clone(), kc0.clone(), vc0.clone()
+        ops.qkv_rope_split(qkv, q_h, kh, vh, pos, Hq, Hkv, base)
+        pdev = torch.tensor([pos], dtype=torch.int32, device="cuda")
+        ops.qkv_rope_split(qkv, q_d, kd, vd, pdev, Hq, Hkv, base)
+        assert torch.equal(q_h, q_d) and torch.equal(kh, kd) and torch.equal(vh, vd)
+        o_h = ops.decode_attention(q_h.view(B, Hq, D), kh, vh, pos + 1)
+        o_d = ops.decode_attention(q_d.view(B, Hq, D), kd, vd, L, n_past=pdev)
+        assert torch.equal(o_h, o_d)
+    # past the cache: q is formed, the cache is untouched
+    kd, vd = kc0.clone(), vc0.clone()
+    q_d = torch.empty((B, Hq, 1, D), dtype=dtype, device="cuda")
+    ops.qkv_rope_split(qkv, q_d, kd, vd, torch.tensor([L], dtype=torch.int32, device="cuda"),
+                       Hq, Hkv, base)
+    torch.cuda.synchronize()
+    assert torch.equal(kd, kc0) and torch.equal(vd, vc0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_generate_graph_equals_eager(cuda, dtype):
+    """Greedy ids from the decode step captured in a HIP graph and replayed
+    (8 replays, eager work between them) == ids from the eager decode loop."""
+    cfg = llama.LlamaConfig(d_model=256, n_heads=4, n_layers=2, vocab_size=512, eps=1e-5,
+                            rope_base=1e4, intermediate_size=512, n_kv_heads_=2)
+    w = llama.init_weights(cfg, dtype=dtype, std=0.2, seed=23)
+    model = llama.Llama(cfg, w)
+    prompt = torch.randint(0, 512, (3, 9), generator=torch.Generator(device="cuda").manual_seed(24),
+                           device="cuda")
+    eager = model.generate(prompt, 10)
+    graph = model.generate_graph(prompt, 10)
+    assert torch.equal(eager, graph), (eager, graph)
