@@ -253,6 +253,44 @@ int teeny_decode_attention_dev(const void* q, const void* k_cache, const void* v
 int teeny_argmax_rows(const void* x, int64_t* out, int rows, int cols, int dtype,
                       hipStream_t stream);
 
+/* Decode-step linear layer y[M, N] = x[M, K] . w[N, K]^T, bf16 only, for
+ * 1 <= M <= 16 (one token per sequence): replaces the external teeny-core
+ * Linear behind sym_linear (src/layers/mod.rs:54-58) at the shapes a KV-cached
+ * decode step has.  Requires N % 64 == 0 and K % 128 == 0; other shapes return
+ * TEENY_ERR_UNSUPPORTED (the caller then uses a general GEMM).  Deterministic.
+ * teeny_linear_swiglu_bf16: w is the fused gate_up weight [2F, K] (gate rows
+ * first, src/loader.rs:49-55), F % 32 == 0; writes y[M, F] =
+ * silu(x w_gate^T) * (x w_up^T) with both products rounded to bf16 first, as
+ * FeedForward's gate_up Linear followed by SwigluOp computes it
+ * (src/layers/ffn.rs:47-56). */
+int teeny_linear_bf16(const void* x, const void* w, void* y, int M, int N, int K,
+                      hipStream_t stream);
+int teeny_linear_swiglu_bf16(const void* x, const void* w, void* y, int M, int F, int K,
+                             hipStream_t stream);
+
+/* The same product split over K for more parallelism at small N: writes
+ * teeny_linear_partials_count(K, k_split) fp32 slabs parts[n][M][N], slab i
+ * summing k in [i k_split, (i+1) k_split).  k_split is a multiple of 512 or
+ * >= K.  The slabs are consumed, summed in slab order and rounded to the
+ * activation dtype (as the unsplit product would be stored), by
+ * teeny_fused_add_rmsnorm_partials_fwd (x = the sum; otherwise as
+ * teeny_fused_add_rmsnorm_fwd, src/kernels/fused_add_rmsnorm.rs:53-110) and
+ * teeny_qkv_rope_split_partials_dev (qkv = the sum; otherwise as
+ * teeny_qkv_rope_split_dev).  No reference counterpart: the reference has no
+ * decode path with a KV cache. */
+int teeny_linear_partials_count(int K, int k_split);
+int teeny_linear_partials_bf16(const void* x, const void* w, float* parts, int M, int N, int K,
+                               int k_split, hipStream_t stream);
+int teeny_fused_add_rmsnorm_partials_fwd(const float* parts, int n_parts, const void* residual,
+                                         void* y, void* h, float* rstd, const void* weight,
+                                         int M, int N, float eps, int dtype,
+                                         hipStream_t stream);
+int teeny_qkv_rope_split_partials_dev(const float* parts, int n_parts, void* q_out,
+                                      void* k_cache, void* v_cache, int batch, int seq_len,
+                                      const int32_t* pos0, int cache_len, int n_heads_q,
+                                      int n_heads_kv, int head_dim, float ln_rope_base,
+                                      int dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

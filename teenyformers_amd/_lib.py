@@ -66,6 +66,13 @@ _SIGNATURES = {
     "teeny_decode_attention_dev": ([_p] * 4 + [_i] * 3 + [_p] + [_i] * 3
                                    + [_f, _i, _p, _sz, _p], _i),
     "teeny_argmax_rows": ([_p, _p, _i, _i, _i, _p], _i),
+    "teeny_linear_bf16": ([_p, _p, _p, _i, _i, _i, _p], _i),
+    "teeny_linear_swiglu_bf16": ([_p, _p, _p, _i, _i, _i, _p], _i),
+    "teeny_linear_partials_count": ([_i, _i], _i),
+    "teeny_linear_partials_bf16": ([_p, _p, _p, _i, _i, _i, _i, _p], _i),
+    "teeny_fused_add_rmsnorm_partials_fwd": ([_p, _i, _p, _p, _p, _p, _p, _i, _i, _f, _i, _p], _i),
+    "teeny_qkv_rope_split_partials_dev": ([_p, _i, _p, _p, _p, _i, _i, _p, _i, _i, _i, _i, _f,
+                                           _i, _p], _i),
 }
 
 

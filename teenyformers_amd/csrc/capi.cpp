@@ -33,7 +33,8 @@
   X(fa2_fwd_bf16)        \
   X(fa2_bwd_bf16)        \
   X(llama)               \
-  X(decode_bf16)
+  X(decode_bf16)         \
+  X(linear_bf16)
 
 #define TEENY_CO_DECL(n) \
   extern "C" const unsigned char teeny_co_##n[]; \
@@ -503,9 +504,34 @@ static int norm_fwd_impl(const void* x, const void* res, void* y, void* h, float
   int vec, ch;
   if (!norm_shape(N, dtype, &vec, &ch)) return TEENY_ERR_UNSUPPORTED;
   char name[64];
-  snprintf(name, sizeof name, "teeny_rmsnorm_fwd_%s_v%d_c%d", dtype_tag(dtype), vec, ch);
   void* args[] = {&x, &res, &y, &h, &rstd, &w, &M, &N, &eps};
+  // Fewer rows than CUs: a workgroup per row (4 wavefronts share a row)
+  // when the row is vectorised and fits 256 threads x 4 vectors.
+  if (M < 256 && vec > 1 && ch <= 16) {
+    snprintf(name, sizeof name, "teeny_rmsnorm_fwd_wg_%s_v%d_c%d", dtype_tag(dtype), vec,
+             ch <= 4 ? 1 : ch / 4);
+    return launch(name, dim3(M), dim3(256), 0, stream, args);
+  }
+  snprintf(name, sizeof name, "teeny_rmsnorm_fwd_%s_v%d_c%d", dtype_tag(dtype), vec, ch);
   return launch(name, dim3((M + 3) / 4), dim3(256), 0, stream, args);
+}
+
+int teeny_fused_add_rmsnorm_partials_fwd(const float* parts, int n_parts, const void* residual,
+                                         void* y, void* h, float* rstd, const void* weight,
+                                         int M, int N, float eps, int dtype,
+                                         hipStream_t stream) {
+  if (!parts || !residual || !y || !h || !weight) return TEENY_ERR_NULL_POINTER;
+  if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
+  if (M <= 0 || N <= 0 || n_parts <= 0 || (long)n_parts * M * N >= kMaxElems)
+    return TEENY_ERR_INVALID_SHAPE;
+  if (!(eps >= 0.0f) || !std::isfinite(eps)) return TEENY_ERR_INVALID_VALUE;
+  int vec, ch;
+  if (!norm_shape(N, dtype, &vec, &ch) || vec == 1) return TEENY_ERR_UNSUPPORTED;
+  char name[64];
+  snprintf(name, sizeof name, "teeny_addnorm_parts_fwd_%s_v%d_c%d", dtype_tag(dtype), vec,
+           ch <= 4 ? 1 : ch / 4);
+  void* args[] = {&parts, &n_parts, &residual, &y, &h, &rstd, &weight, &M, &N, &eps};
+  return launch(name, dim3(M), dim3(256), 0, stream, args);
 }
 
 int teeny_fused_add_rmsnorm_fwd(const void* x, const void* residual, void* y, void* h,
@@ -594,10 +620,10 @@ int teeny_swiglu_bwd(const void* grad, const void* z, void* dz, int M, int d_ff,
   return swiglu_impl(true, grad, z, dz, M, d_ff, dtype, stream);
 }
 
-static int qkv_rope_split_impl(const void* qkv, void* q_out, void* k_cache, void* v_cache,
-                               int batch, int seq_len, const int32_t* pos_dev, int pos0,
-                               int cache_len, int n_heads_q, int n_heads_kv, int head_dim,
-                               float ln_rope_base, int dtype, hipStream_t stream) {
+static int qkv_rope_split_check(const void* qkv, const void* q_out, const void* k_cache,
+                                const void* v_cache, int batch, int seq_len, int pos0,
+                                int cache_len, int n_heads_q, int n_heads_kv, int head_dim,
+                                float ln_rope_base, int dtype) {
   if (!qkv || !q_out || !k_cache || !v_cache) return TEENY_ERR_NULL_POINTER;
   if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
   if (batch <= 0 || seq_len <= 0 || pos0 < 0 || n_heads_q <= 0 || n_heads_kv <= 0 ||
@@ -608,6 +634,18 @@ static int qkv_rope_split_impl(const void* qkv, void* q_out, void* k_cache, void
   const int vn = dtype == TEENY_BF16 ? 8 : 4;
   if (head_dim % vn != 0 || head_dim % 2 != 0) return TEENY_ERR_UNSUPPORTED;
   if (!std::isfinite(ln_rope_base)) return TEENY_ERR_INVALID_VALUE;
+  if ((long)batch * ((n_heads_q + 2 * n_heads_kv + 15) / 16) > 65535)
+    return TEENY_ERR_INVALID_SHAPE;
+  return TEENY_OK;
+}
+
+static int qkv_rope_split_impl(const void* qkv, void* q_out, void* k_cache, void* v_cache,
+                               int batch, int seq_len, const int32_t* pos_dev, int pos0,
+                               int cache_len, int n_heads_q, int n_heads_kv, int head_dim,
+                               float ln_rope_base, int dtype, hipStream_t stream) {
+  int rc = qkv_rope_split_check(qkv, q_out, k_cache, v_cache, batch, seq_len, pos0, cache_len,
+                                n_heads_q, n_heads_kv, head_dim, ln_rope_base, dtype);
+  if (rc) return rc;
   const int htot = n_heads_q + 2 * n_heads_kv;
   const long gy = (long)batch * ((htot + 15) / 16);
   if (gy > 65535) return TEENY_ERR_INVALID_SHAPE;
@@ -634,6 +672,33 @@ int teeny_qkv_rope_split_dev(const void* qkv, void* q_out, void* k_cache, void* 
   if (!pos0) return TEENY_ERR_NULL_POINTER;
   return qkv_rope_split_impl(qkv, q_out, k_cache, v_cache, batch, seq_len, pos0, 0, cache_len,
                              n_heads_q, n_heads_kv, head_dim, ln_rope_base, dtype, stream);
+}
+
+int teeny_qkv_rope_split_partials_dev(const float* parts, int n_parts, void* q_out,
+                                      void* k_cache, void* v_cache, int batch, int seq_len,
+                                      const int32_t* pos0, int cache_len, int n_heads_q,
+                                      int n_heads_kv, int head_dim, float ln_rope_base,
+                                      int dtype, hipStream_t stream) {
+  if (!parts || !pos0) return TEENY_ERR_NULL_POINTER;
+  if (n_parts <= 0) return TEENY_ERR_INVALID_SHAPE;
+  // shape checks on a stand-in qkv pointer, then the partial-input kernel
+  int rc = qkv_rope_split_check(parts, q_out, k_cache, v_cache, batch, seq_len, 0, cache_len,
+                                n_heads_q, n_heads_kv, head_dim, ln_rope_base, dtype);
+  if (rc) return rc;
+  const int htot = n_heads_q + 2 * n_heads_kv;
+  long part_stride = (long)batch * seq_len * htot * head_dim;
+  if (part_stride * n_parts >= kMaxElems || (long)batch * ((htot + 3) / 4) > 65535)
+    return TEENY_ERR_INVALID_SHAPE;
+  char name[48];
+  snprintf(name, sizeof name, "teeny_qkv_parts_rope_split_%s", dtype_tag(dtype));
+  int pos_imm = 0;
+  void* args[] = {&parts,     &n_parts,   &part_stride, &q_out,      &k_cache,
+                  &v_cache,   &seq_len,   &pos0,        &pos_imm,    &cache_len,
+                  &n_heads_q, &n_heads_kv, &head_dim,   &ln_rope_base};
+  // 4 head rows x 4 positions per workgroup (the partial-input kernel's tile)
+  unsigned shmem = 4u * (unsigned)(head_dim / 2) * 8u;
+  return launch(name, dim3((seq_len + 3) / 4, (unsigned)((long)batch * ((htot + 3) / 4))),
+                dim3(256), shmem, stream, args);
 }
 
 static int decode_chunks(int n_keys) { return (n_keys + 255) / 256; }  // fp32 kernel
@@ -736,6 +801,51 @@ int teeny_argmax_rows(const void* x, int64_t* out, int rows, int cols, int dtype
   snprintf(name, sizeof name, "teeny_argmax_rows_%s", dtype_tag(dtype));
   void* args[] = {&x, &out, &cols};
   return launch(name, dim3(rows), dim3(1024), 0, stream, args);
+}
+
+// Decode-step linear layers (linear_bf16.hip): 64 W rows per workgroup
+// (32 gate + 32 up rows for SwiGLU), x staged in 512-wide K chunks.
+static int linear_sk_check(const void* x, const void* w, const void* y, int M, int N, int K,
+                           long w_rows, int row_tile) {
+  if (!x || !w || !y) return TEENY_ERR_NULL_POINTER;
+  if (M <= 0 || N <= 0 || K <= 0 || w_rows * K >= kMaxElems * 2) return TEENY_ERR_INVALID_SHAPE;
+  if (M > 16 || N % row_tile != 0 || K % 128 != 0) return TEENY_ERR_UNSUPPORTED;
+  return TEENY_OK;
+}
+
+int teeny_linear_bf16(const void* x, const void* w, void* y, int M, int N, int K,
+                      hipStream_t stream) {
+  int rc = linear_sk_check(x, w, y, M, N, K, N, 64);
+  if (rc) return rc;
+  void* args[] = {&x, &w, &y, &M, &N, &K};
+  return launch("teeny_linear_sk_bf16", dim3(N / 64), dim3(256), 0, stream, args);
+}
+
+int teeny_linear_swiglu_bf16(const void* x, const void* w, void* y, int M, int F, int K,
+                             hipStream_t stream) {
+  int rc = linear_sk_check(x, w, y, M, F, K, 2L * F, 32);
+  if (rc) return rc;
+  void* args[] = {&x, &w, &y, &M, &F, &K};
+  return launch("teeny_linear_sk_swiglu_bf16", dim3(F / 32), dim3(256), 0, stream, args);
+}
+
+int teeny_linear_partials_count(int K, int k_split) {
+  if (K <= 0 || k_split <= 0) return 0;
+  if (k_split >= K) return 1;
+  return (K + k_split - 1) / k_split;
+}
+
+int teeny_linear_partials_bf16(const void* x, const void* w, float* parts, int M, int N, int K,
+                               int k_split, hipStream_t stream) {
+  int rc = linear_sk_check(x, w, parts, M, N, K, N, 64);
+  if (rc) return rc;
+  if (k_split <= 0) return TEENY_ERR_INVALID_VALUE;
+  if (k_split >= K) k_split = K;
+  else if (k_split % 512 != 0) return TEENY_ERR_INVALID_VALUE;  // whole staged x chunks
+  const int n = teeny_linear_partials_count(K, k_split);
+  if (n > 65535) return TEENY_ERR_INVALID_SHAPE;
+  void* args[] = {&x, &w, &parts, &M, &N, &K, &k_split};
+  return launch("teeny_linear_sk_part_bf16", dim3(N / 64, n), dim3(256), 0, stream, args);
 }
 
 int teeny_token_embed_fwd(const void* ids, const void* weight, void* out, int seq_len,

@@ -73,6 +73,43 @@ template <> struct Vec16<bf16> {
   }
 };
 
+// VEC consecutive values of a sum of n fp32 partial slabs (slab s at
+// part + s * stride), added in slab order and rounded to T: what a product
+// split over K gives once its parts are summed and stored in T.
+template <typename T, int VEC>
+DEVI void ld_parts(const float* __restrict__ part, long stride, int n, float* out) {
+  static_assert(VEC % 4 == 0, "16-byte loads");
+  constexpr int U = 8;  // slabs whose loads are in flight together
+  float acc[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) acc[j] = 0.0f;
+  int s = 0;
+  for (; s + U <= n; s += U) {
+    f32x4 v[U][VEC / 4];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < VEC / 4; ++j)
+        v[u][j] = *reinterpret_cast<const f32x4*>(part + (s + u) * stride + 4 * j);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < VEC / 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[4 * j + i] += v[u][j][i];
+  }
+  for (; s < n; ++s) {
+#pragma unroll
+    for (int j = 0; j < VEC / 4; ++j) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(part + s * stride + 4 * j);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[4 * j + i] += v[i];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) out[j] = (float)(T)acc[j];
+}
+
 // Wavefront (64-lane) reductions through DPP/permute, all lanes get the result.
 DEVI float wave_sum(float v) {
 #pragma unroll

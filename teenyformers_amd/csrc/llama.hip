@@ -21,46 +21,71 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kPos = 16;    // positions per workgroup
-constexpr int kRows = 16;   // head rows (of Hq + 2 Hkv) per workgroup
+// A workgroup covers kRows head rows (of Hq + 2 Hkv) x kPos positions: 16 x 16
+// for a prompt; 4 x 4 for the few rows of a decode step, whose QKV comes as
+// K-split slabs, so that 12x more workgroups share the slab reads.
 
-template <typename T>
+// PARTS: qkv is the sum of n_parts fp32 slabs part_stride apart (the QKV
+// projection split over K), rounded to T as the unsplit product is stored.
+template <typename T, bool PARTS = false, int kRows = 16, int kPos = 16>
 __device__ void qkv_rope_split(const T* __restrict__ qkv, T* __restrict__ q_out,
                                T* __restrict__ k_cache, T* __restrict__ v_cache, int seq,
                                const int* __restrict__ pos_dev, int pos0, int cache_len, int hq,
-                               int hkv, int head_dim, float ln_base) {
+                               int hkv, int head_dim, float ln_base,
+                               const float* __restrict__ parts = nullptr, int n_parts = 0,
+                               long part_stride = 0) {
   extern __shared__ float2 cs_tab[];  // [kPos][head_dim / 2]
-  if (pos_dev) pos0 += *pos_dev;
   const int half = head_dim / 2;
   const int s0 = blockIdx.x * kPos;
   const int htot = hq + 2 * hkv;
   const int rows_per_b = (htot + kRows - 1) / kRows;
   const int b = blockIdx.y / rows_per_b;
   const int h0 = (blockIdx.y - b * rows_per_b) * kRows;
+  constexpr int VN = Vec16<T>::N;
+  const int vpr = head_dim / VN;
+  const int total = kRows * kPos * vpr;
+  auto source = [&](int i, int& v, int& p, int& hh, int& s) {  // false: nothing to do
+    v = i % vpr;
+    const int r = i / vpr;
+    p = r % kPos;
+    hh = h0 + r / kPos;
+    s = s0 + p;
+    return s < seq && hh < htot;
+  };
+  auto load = [&](int v, int hh, int s, float* in) {
+    const long src = ((long)b * seq + s) * htot * head_dim + (long)hh * head_dim + v * VN;
+    if constexpr (PARTS)
+      ld_parts<T, VN>(parts + src, part_stride, n_parts, in);
+    else
+      Vec16<T>::load(qkv + src, in);
+  };
+  // this thread's first item is read before the rotation table is built, so
+  // the two latencies overlap (a decode step has one item per thread)
+  int v, p, hh, s;
+  float in[VN];
+  const bool first = (int)threadIdx.x < total && source(threadIdx.x, v, p, hh, s);
+  if (first) load(v, hh, s, in);
+
+  if (pos_dev) pos0 += *pos_dev;
   const float c = (-2.0f * ln_base) / (float)head_dim;
   for (int i = threadIdx.x; i < kPos * half; i += kThreads) {
-    int p = i / half, k = i - p * half;
-    if (s0 + p >= seq) break;  // i grows with p: no later entry is needed either
+    int pp = i / half, k = i - pp * half;
+    if (s0 + pp >= seq) break;  // i grows with pp: no later entry is needed either
     float inv = (float)exp((double)((float)k * c));
-    float theta = (float)(pos0 + s0 + p) * inv;
+    float theta = (float)(pos0 + s0 + pp) * inv;
     float sn, cn;
     sincosf(theta, &sn, &cn);
     cs_tab[i] = make_float2(cn, sn);
   }
   __syncthreads();
-  constexpr int VN = Vec16<T>::N;
-  const int vpr = head_dim / VN;
-  const int total = kRows * kPos * vpr;
   for (int i = threadIdx.x; i < total; i += kThreads) {
-    int v = i % vpr;
-    int r = i / vpr;
-    int p = r % kPos;
-    int hh = h0 + r / kPos;
-    int s = s0 + p;
-    if (s >= seq || hh >= htot) continue;
+    if (i != (int)threadIdx.x) {
+      if (!source(i, v, p, hh, s)) continue;
+      load(v, hh, s, in);
+    } else if (!first) {
+      continue;
+    }
     if (hh >= hq && (pos0 + s < 0 || pos0 + s >= cache_len)) continue;  // outside the cache
-    float in[VN];
-    Vec16<T>::load(qkv + ((long)b * seq + s) * htot * head_dim + (long)hh * head_dim + v * VN, in);
     T* dst;
     if (hh < hq)
       dst = q_out + (((long)b * hq + hh) * seq + s) * head_dim;
@@ -303,6 +328,18 @@ __device__ void argmax_rows(const T* __restrict__ x, long long* __restrict__ out
 }
 
 }  // namespace
+
+#define TEENY_QKV_PARTS_INST(TN, T)                                                             \
+  extern "C" __global__ __launch_bounds__(256) void teeny_qkv_parts_rope_split_##TN(           \
+      const float* parts, int n_parts, long part_stride, T* q_out, T* k_cache, T* v_cache,      \
+      int seq, const int* pos_dev, int pos0, int cache_len, int hq, int hkv, int head_dim,      \
+      float ln_base) {                                                                          \
+    qkv_rope_split<T, true, 4, 4>(nullptr, q_out, k_cache, v_cache, seq, pos_dev, pos0,        \
+                                  cache_len, hq, hkv, head_dim, ln_base, parts, n_parts,        \
+                                  part_stride);                                                 \
+  }
+TEENY_QKV_PARTS_INST(f32, float)
+TEENY_QKV_PARTS_INST(bf16, bf16)
 
 #define TEENY_LLAMA_INST(TN, T)                                                                 \
   extern "C" __global__ __launch_bounds__(256) void teeny_qkv_rope_split_##TN(                 \

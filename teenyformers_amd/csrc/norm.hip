@@ -184,6 +184,90 @@ extern "C" __global__ __launch_bounds__(256) void teeny_rmsnorm_dw_reduce_bf16(
   dw[n] = (bf16)((float)dw[n] + s);
 }
 
+// Few rows (a decode step's M = batch): one 256-thread workgroup per row, so
+// a row's loads are spread over four wavefronts instead of serialised in one;
+// the four wavefront sums are added in a fixed order.  PARTS: x is the sum of
+// n_parts fp32 slabs [n_parts][M][N] (a linear layer split over K), rounded
+// to T as the unsplit product would be stored.
+template <typename T, int VEC, int CH, bool PARTS = false>
+__device__ void rmsnorm_fwd_row_wg(const T* __restrict__ x, const T* __restrict__ res,
+                                   T* __restrict__ y, T* __restrict__ h_out,
+                                   float* __restrict__ rstd, const T* __restrict__ w, int N,
+                                   float eps, const float* __restrict__ xparts = nullptr,
+                                   int n_parts = 0) {
+  __shared__ float part[kWaves];
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x;
+  const long base = (long)row * N;
+  float hv[CH][VEC];
+  float sq = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    int idx = (c * 256 + tid) * VEC;
+    if (idx < N) {
+      if constexpr (PARTS)
+        ld_parts<T, VEC>(xparts + base + idx, (long)gridDim.x * N, n_parts, hv[c]);
+      else
+        ldv<T, VEC>(x + base + idx, hv[c]);
+      if (res) {
+        float rv[VEC];
+        ldv<T, VEC>(res + base + idx, rv);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) hv[c][j] += rv[j];
+      }
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) sq += hv[c][j] * hv[c][j];
+      if (h_out) {
+        stv<T, VEC>(h_out + base + idx, hv[c]);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) hv[c][j] = (float)(T)hv[c][j];
+      }
+    }
+  }
+  sq = wave_sum(sq);
+  if ((tid & 63) == 0) part[tid >> 6] = sq;
+  __syncthreads();
+  sq = (part[0] + part[1]) + (part[2] + part[3]);
+  const float rs = 1.0f / sqrtf(sq * (1.0f / (float)N) + eps);
+  if (tid == 0 && rstd) rstd[row] = rs;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    int idx = (c * 256 + tid) * VEC;
+    if (idx < N) {
+      float wv[VEC], out[VEC];
+      ldv<T, VEC>(w + idx, wv);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) out[j] = hv[c][j] * rs * wv[j];
+      stv<T, VEC>(y + base + idx, out);
+    }
+  }
+}
+
+#define TEENY_NORM_WG_INST(TN, T, VEC, CH)                                                      \
+  extern "C" __global__ __launch_bounds__(256) void teeny_rmsnorm_fwd_wg_##TN##_v##VEC##_c##CH( \
+      const T* x, const T* res, T* y, T* h, float* rstd, const T* w, int M, int N, float eps) { \
+    rmsnorm_fwd_row_wg<T, VEC, CH>(x, res, y, h, rstd, w, N, eps);                              \
+  }
+#define TEENY_NORM_PARTS_INST(TN, T, VEC, CH)                                                 \
+  extern "C" __global__ __launch_bounds__(256) void                                            \
+      teeny_addnorm_parts_fwd_##TN##_v##VEC##_c##CH(const float* parts, int n_parts,           \
+                                                    const T* res, T* y, T* h, float* rstd,     \
+                                                    const T* w, int M, int N, float eps) {     \
+    rmsnorm_fwd_row_wg<T, VEC, CH, true>(nullptr, res, y, h, rstd, w, N, eps, parts, n_parts); \
+  }
+TEENY_NORM_PARTS_INST(f32, float, 4, 1)
+TEENY_NORM_PARTS_INST(f32, float, 4, 2)
+TEENY_NORM_PARTS_INST(f32, float, 4, 4)
+TEENY_NORM_PARTS_INST(bf16, bf16, 8, 1)
+TEENY_NORM_PARTS_INST(bf16, bf16, 8, 2)
+TEENY_NORM_PARTS_INST(bf16, bf16, 8, 4)
+TEENY_NORM_WG_INST(f32, float, 4, 1)
+TEENY_NORM_WG_INST(f32, float, 4, 2)
+TEENY_NORM_WG_INST(f32, float, 4, 4)
+TEENY_NORM_WG_INST(bf16, bf16, 8, 1)
+TEENY_NORM_WG_INST(bf16, bf16, 8, 2)
+TEENY_NORM_WG_INST(bf16, bf16, 8, 4)
+
 #define TEENY_NORM_INST(TN, T, VEC, CH)                                                          \
   extern "C" __global__ __launch_bounds__(256) void teeny_rmsnorm_fwd_##TN##_v##VEC##_c##CH(    \
       const T* x, const T* res, T* y, T* h, float* rstd, const T* w, int M, int N, float eps) {  \

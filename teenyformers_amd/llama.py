@@ -30,7 +30,6 @@ import json
 import math
 
 import torch
-import torch.nn.functional as F
 
 from . import ops
 
@@ -130,7 +129,8 @@ class Llama:
         B, S, d = n1.shape
         Hq, Hkv, D = cfg.n_heads, cfg.n_kv_heads(), cfg.head_dim()
         p = f"model.layers.{i}.self_attn."
-        qkv = F.linear(n1, w[p + "qkv_proj.weight"])  # [B, S, (Hq+2Hkv) D]
+        # [B, S, (Hq+2Hkv) D]; K-split fp32 slabs at decode sizes
+        qkv = ops.linear_split(n1, w[p + "qkv_proj.weight"])
         q = torch.empty((B, Hq, S, D), dtype=n1.dtype, device=n1.device)
         ops.qkv_rope_split(qkv, q, cache.k[i], cache.v[i], pos0, Hq, Hkv, cfg.rope_base)
         scale = cfg.softmax_scale()
@@ -149,7 +149,9 @@ class Llama:
                 raise ValueError("prefill must start at position 0")
             # causal FA2 over the cache: keys past S are masked (key > query)
             o, _ = ops.flash_attn2_fwd(q, cache.k[i], cache.v[i], scale, causal=True)
-        return F.linear(ops.merge_heads(o), w[p + "o_proj.weight"])
+        # one position: [B, Hq, 1, D] is already the merged [B, 1, Hq D] layout
+        att = o.view(B, S, Hq * D) if S == 1 else ops.merge_heads(o)
+        return ops.linear_split(att, w[p + "o_proj.weight"])
 
     def _decode_ws(self, B: int, cache: KVCache, device) -> torch.Tensor:
         """Split-K workspace for decode attention over the whole cache."""
@@ -162,8 +164,8 @@ class Llama:
     def _ffn(self, i: int, n2: torch.Tensor) -> torch.Tensor:
         """src/layers/ffn.rs:47-56."""
         p = f"model.layers.{i}.mlp."
-        z = F.linear(n2, self.w[p + "gate_up_proj.weight"])
-        return F.linear(ops.swiglu(z), self.w[p + "down_proj.weight"])
+        f = ops.linear_swiglu(n2, self.w[p + "gate_up_proj.weight"])
+        return ops.linear_split(f, self.w[p + "down_proj.weight"])
 
     def hidden(self, ids: torch.Tensor, cache: KVCache, pos0) -> torch.Tensor:
         """Final-norm hidden states [B, S, d] for ids [B, S] at positions pos0..,
@@ -189,7 +191,7 @@ class Llama:
 
     def logits(self, h: torch.Tensor) -> torch.Tensor:
         """Tied lm_head (src/layers/embedding.rs:159-167): h @ E^T."""
-        return F.linear(h, self.w["model.embed_tokens.weight"])
+        return ops.linear(h, self.w["model.embed_tokens.weight"])
 
     def forward(self, ids: torch.Tensor) -> torch.Tensor:
         """All-position logits [B, S, vocab] (src/llama.rs:65-81)."""

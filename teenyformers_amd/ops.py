@@ -220,7 +220,19 @@ def _rows(x: torch.Tensor):
 
 
 def fused_add_rmsnorm(x, residual, weight, eps: float):
-    """h = x + residual; y = h * rsqrt(mean(h^2) + eps) * weight -> (y, h, rstd)."""
+    """h = x + residual; y = h * rsqrt(mean(h^2) + eps) * weight -> (y, h, rstd).
+    x may be Partials (summed and rounded to residual's dtype first)."""
+    if isinstance(x, Partials):
+        _dev(x.slabs, residual, weight)
+        M, N = _rows(residual)
+        if x.slabs.shape[1:] != (M, N) or x.dtype != residual.dtype:
+            raise ValueError("fused_add_rmsnorm: partial slabs do not match the residual")
+        y = torch.empty_like(residual)
+        h = torch.empty_like(residual)
+        rstd = torch.empty(M, dtype=torch.float32, device=residual.device)
+        call("teeny_fused_add_rmsnorm_partials_fwd", _p(x.slabs), x.n, _p(residual), _p(y),
+             _p(h), _p(rstd), _p(weight), M, N, float(eps), _code(residual), _stream())
+        return y, h, rstd
     _dev(x, residual, weight)
     M, N = _rows(x)
     y = torch.empty_like(x)
@@ -340,6 +352,18 @@ def qkv_rope_split(qkv, q_out, k_cache, v_cache, pos0, n_heads_q: int, n_heads_k
     written to caches [B, Hkv, L, D] at rows pos0 .. pos0+S-1.  pos0: an int,
     or a one-element int32 device tensor read when the kernel runs (for
     captured graphs)."""
+    if isinstance(qkv, Partials):
+        _dev(qkv.slabs, q_out, k_cache, v_cache)
+        B, S, _ = qkv.shape
+        D = q_out.shape[-1]
+        if not isinstance(pos0, torch.Tensor):
+            pos0 = torch.tensor([pos0], dtype=torch.int32, device=q_out.device)
+        elif pos0.dtype != torch.int32 or not pos0.is_cuda:
+            raise TypeError("a device position must be an int32 CUDA tensor")
+        call("teeny_qkv_rope_split_partials_dev", _p(qkv.slabs), qkv.n, _p(q_out), _p(k_cache),
+             _p(v_cache), B, S, _p(pos0), k_cache.shape[2], n_heads_q, n_heads_kv, D,
+             _ln(rope_base), _code(q_out), _stream())
+        return
     _dev(qkv, q_out, k_cache, v_cache)
     B, S, _ = qkv.shape
     D = q_out.shape[-1]
@@ -390,3 +414,88 @@ def argmax_rows(x, out=None):
     out = torch.empty(rows, dtype=torch.int64, device=x.device) if out is None else out
     call("teeny_argmax_rows", _p(x2), _p(out), rows, cols, _code(x2), _stream())
     return out
+
+
+def _skinny(x2: torch.Tensor, w: torch.Tensor, n_out: int, row_tile: int = 64) -> bool:
+    """Shapes the decode-step linear kernels take (else a general GEMM runs)."""
+    M, K = x2.shape
+    if torch.is_grad_enabled() and (x2.requires_grad or w.requires_grad):
+        return False  # the kernels have no backward
+    return (x2.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x2.is_cuda
+            and 1 <= M <= 16 and K % 128 == 0 and n_out % row_tile == 0 and w.is_contiguous())
+
+
+def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """y = x w^T (src/layers/mod.rs:54-58; w [out, in]).  Up to 16 rows of
+    bf16 run the weight-streaming decode kernel; larger M is a GEMM for the
+    matrix-core GEMM library (hipBLASLt through torch)."""
+    x2 = x.reshape(-1, x.shape[-1])
+    N, K = w.shape
+    if K != x2.shape[1]:
+        raise ValueError(f"linear: x has {x2.shape[1]} features, w expects {K}")
+    if not _skinny(x2, w, N):
+        return torch.nn.functional.linear(x, w)
+    x2 = x2.contiguous()
+    y = torch.empty((x2.shape[0], N), dtype=x.dtype, device=x.device)
+    call("teeny_linear_bf16", _p(x2), _p(w), _p(y), x2.shape[0], N, K, _stream())
+    return y.view(*x.shape[:-1], N)
+
+
+def linear_swiglu(x: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
+    """swiglu(x w_gate_up^T) (src/layers/ffn.rs:47-56): fused in one kernel for
+    up to 16 bf16 rows, else the GEMM followed by the SwiGLU kernel."""
+    x2 = x.reshape(-1, x.shape[-1])
+    N2, K = w_gate_up.shape
+    if K != x2.shape[1] or N2 % 2:
+        raise ValueError("linear_swiglu: weight must be [2F, in] with in = x's features")
+    F = N2 // 2
+    if not _skinny(x2, w_gate_up, F, row_tile=32):
+        return swiglu(torch.nn.functional.linear(x, w_gate_up))
+    x2 = x2.contiguous()
+    y = torch.empty((x2.shape[0], F), dtype=x.dtype, device=x.device)
+    call("teeny_linear_swiglu_bf16", _p(x2), _p(w_gate_up), _p(y), x2.shape[0], F, K, _stream())
+    return y.view(*x.shape[:-1], F)
+
+
+class Partials:
+    """A linear layer's output left as fp32 slabs [n, M, N] of a K split; the
+    consumer (fused_add_rmsnorm, qkv_rope_split) sums them in slab order and
+    rounds to `dtype`, the product's storage type."""
+
+    def __init__(self, slabs: torch.Tensor, shape, dtype):
+        self.slabs, self.shape, self.dtype = slabs, tuple(shape), dtype
+
+    @property
+    def n(self) -> int:
+        return self.slabs.shape[0]
+
+    def sum(self) -> torch.Tensor:
+        """The product itself (for checks; consumers read the slabs)."""
+        return self.slabs.sum(0, dtype=torch.float32).to(self.dtype).view(self.shape)
+
+
+def _k_split(N: int, K: int) -> int:
+    """K per slab: about 384 workgroups of 64 features in all (each slab costs
+    the consumer a read), 512-wide chunks."""
+    groups = N // 64
+    splits = max(1, min(K // 512, -(-384 // groups)))
+    per = -(-K // splits)
+    return -(-per // 512) * 512
+
+
+def linear_split(x: torch.Tensor, w: torch.Tensor):
+    """x w^T as Partials where the decode kernels take the shape (up to 16
+    bf16 rows), else the GEMM's tensor."""
+    x2 = x.reshape(-1, x.shape[-1])
+    N, K = w.shape
+    if K != x2.shape[1]:
+        raise ValueError(f"linear: x has {x2.shape[1]} features, w expects {K}")
+    if not _skinny(x2, w, N):
+        return torch.nn.functional.linear(x, w)
+    x2 = x2.contiguous()
+    ks = _k_split(N, K) if K >= 1024 else K
+    n = _lib.lib().teeny_linear_partials_count(K, ks)
+    slabs = torch.empty((n, x2.shape[0], N), dtype=torch.float32, device=x.device)
+    call("teeny_linear_partials_bf16", _p(x2), _p(w), _p(slabs), x2.shape[0], N, K, ks,
+         _stream())
+    return Partials(slabs, (*x.shape[:-1], N), x.dtype)

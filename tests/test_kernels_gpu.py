@@ -137,7 +137,7 @@ def test_rmsnorm_f32_fwd_bwd(cuda, m, n):
     assert np.abs(host(dwp) - dwpe).max() <= 1e-5 * max(1.0, np.abs(dwpe).max())
 
 
-@pytest.mark.parametrize("m,n", [(8192, 2048), (100, 4096)])
+@pytest.mark.parametrize("m,n", [(8192, 2048), (100, 4096), (16, 8192), (1, 1024)])
 def test_rmsnorm_bf16(cuda, m, n):
     x = O.bf16_round(randn(9, m, n))
     r = O.bf16_round(randn(10, m, n))

@@ -214,3 +214,93 @@ def test_generate_graph_equals_eager(cuda, dtype):
     eager = model.generate(prompt, 10)
     graph = model.generate_graph(prompt, 10)
     assert torch.equal(eager, graph), (eager, graph)
+
+
+def _bf16_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda", torch.bfloat16)
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (1, 64, 128), (5, 192, 256),        # one partial 512-wide x chunk
+    (16, 4096, 4096), (16, 64, 14336),  # decode shapes: o_proj, down
+    (3, 1024, 640), (16, 128, 4224)])   # a last chunk of one 128-wide step
+def test_linear_skinny(cuda, M, N, K):
+    """Decode-step linear against float64 matmul of the same bf16 operands:
+    within one bf16 rounding of the output (summation order differs)."""
+    rng = np.random.default_rng(M * 7919 + N + K)
+    x = O.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    w = O.bf16_round((0.02 * rng.standard_normal((N, K))).astype(np.float32))
+    y = ops.linear(_bf16_dev(x), _bf16_dev(w))
+    want = x.astype(np.float64) @ w.astype(np.float64).T
+    err = np.abs(host(y) - want)
+    assert np.all(err <= np.abs(want) * 2.0 ** -8 + 1e-4 * np.abs(want).max()), err.max()
+    # deterministic: the same bits on a second call
+    assert torch.equal(y, ops.linear(_bf16_dev(x), _bf16_dev(w)))
+    # the K-split form: slabs sum to the same product
+    part = ops.linear_split(_bf16_dev(x), _bf16_dev(w))
+    slabs = part.slabs.cpu().numpy()
+    tot = slabs.sum(0, dtype=np.float64)
+    assert np.all(np.abs(tot - want) <= np.abs(want) * 2.0 ** -16 + 1e-5 * np.abs(want).max())
+
+
+def _seq_sum_bf16(slabs):
+    """Slab-order fp32 sum rounded to bf16, as the consumers add them."""
+    acc = np.zeros(slabs.shape[1:], np.float32)
+    for s in slabs:
+        acc = (acc + s).astype(np.float32)
+    return O.bf16_round(acc)
+
+
+def test_partials_consumers_bit_exact(cuda):
+    """The residual-add norm and the QKV split read K-split slabs exactly as
+    they read the stored bf16 product."""
+    rng = np.random.default_rng(11)
+    B, Hq, Hkv, D, L = 4, 8, 2, 64, 64
+    d = 1024
+    n = (Hq + 2 * Hkv) * D
+    x = _bf16_dev(rng.standard_normal((B, d)).astype(np.float32))
+    wq = _bf16_dev((0.02 * rng.standard_normal((n, d))).astype(np.float32))
+    wo = _bf16_dev((0.02 * rng.standard_normal((d, d))).astype(np.float32))
+    res = _bf16_dev(rng.standard_normal((B, d)).astype(np.float32))
+    gamma = _bf16_dev((1 + 0.1 * rng.standard_normal(d)).astype(np.float32))
+    po = ops.linear_split(x, wo)
+    assert po.n == 2
+    a = _bf16_dev(_seq_sum_bf16(po.slabs.cpu().numpy()))
+    y1, h1, r1 = ops.fused_add_rmsnorm(po, res, gamma, 1e-5)
+    y2, h2, r2 = ops.fused_add_rmsnorm(a, res, gamma, 1e-5)
+    assert torch.equal(y1, y2) and torch.equal(h1, h2) and torch.equal(r1, r2)
+    pq = ops.linear_split(x.view(B, 1, d), wq)
+    qkv = _bf16_dev(_seq_sum_bf16(pq.slabs.cpu().numpy())).view(B, 1, n)
+    pos = torch.tensor([17], dtype=torch.int32, device="cuda")
+    outs = []
+    for src in (pq, qkv):
+        q = torch.zeros((B, Hq, 1, D), dtype=torch.bfloat16, device="cuda")
+        kc = torch.zeros((B, Hkv, L, D), dtype=torch.bfloat16, device="cuda")
+        vc = torch.zeros_like(kc)
+        ops.qkv_rope_split(src, q, kc, vc, pos, Hq, Hkv, 5e5)
+        outs.append((q, kc, vc))
+    for t1, t2 in zip(*outs):
+        assert torch.equal(t1, t2)
+
+
+@pytest.mark.parametrize("M,F,K", [(16, 14336 // 8, 4096), (2, 64, 640)])
+def test_linear_swiglu_skinny(cuda, M, F, K):
+    """Fused gate_up product + SwiGLU against the unfused composition: the
+    float64 product rounded to bf16, then the oracle's SwiGLU."""
+    rng = np.random.default_rng(F + K)
+    x = O.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    w = O.bf16_round((0.02 * rng.standard_normal((2 * F, K))).astype(np.float32))
+    y = ops.linear_swiglu(_bf16_dev(x), _bf16_dev(w))
+    z = O.bf16_round((x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32))
+    want = O.bf16_round(O.swiglu_fwd(z))
+    err = np.abs(host(y) - want)
+    # one bf16 step of z can move silu(g) * u by a few output ulps
+    assert np.all(err <= np.abs(want) * 2.0 ** -5 + 1e-3 * np.abs(want).max()), err.max()
+    assert rel_l2(host(y), want) <= 5e-3
+
+
+def test_linear_large_m_uses_gemm(cuda):
+    """More than 16 rows is a general GEMM (same product, torch's library)."""
+    x = torch.randn((17, 256), device="cuda", dtype=torch.bfloat16)
+    w = torch.randn((32, 256), device="cuda", dtype=torch.bfloat16)
+    assert torch.equal(ops.linear(x, w), torch.nn.functional.linear(x, w))
