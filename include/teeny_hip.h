@@ -247,9 +247,10 @@ int teeny_decode_attention_dev(const void* q, const void* k_cache, const void* v
                                int dtype, void* workspace, size_t workspace_bytes,
                                hipStream_t stream);
 
-/* Row argmax of x [rows, cols] -> out[rows] (int64): the first index of the
- * maximum, NaN counting as the maximum (torch.argmax's convention); the
- * reference's greedy choice (examples/llama_generate.rs:252-257). */
+/* Row argmax of x [rows, cols] -> out[rows] (int64): the reference's greedy
+ * choice (examples/llama_generate.rs:252-257), the LAST index among equal
+ * maxima (Rust's Iterator::max_by); NaN, on which the reference's comparison
+ * panics, counts as the maximum (the last NaN wins). */
 int teeny_argmax_rows(const void* x, int64_t* out, int rows, int cols, int dtype,
                       hipStream_t stream);
 

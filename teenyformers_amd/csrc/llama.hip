@@ -267,7 +267,9 @@ __device__ void decode_combine(const float* __restrict__ pm, const float* __rest
 }
 
 // Row argmax: one workgroup of 1024 threads per row, 16-byte loads; the
-// first index of the maximum (NaN counts as the maximum), as torch.argmax.
+// last index of the maximum, as the reference's greedy_sample
+// (examples/llama_generate.rs:252-257, Iterator::max_by); NaN, on which the
+// reference's comparison panics, counts as the maximum.
 constexpr int kArgThreads = 1024;
 template <typename T>
 __device__ void argmax_rows(const T* __restrict__ x, long long* __restrict__ out, int cols) {
@@ -275,12 +277,13 @@ __device__ void argmax_rows(const T* __restrict__ x, long long* __restrict__ out
   __shared__ int bi[kArgThreads / 64];
   const T* row = x + (long)blockIdx.x * cols;
   float v = -INFINITY;
-  int idx = 0x7fffffff;
-  // a beats b: larger, or NaN over a number, or equal with the smaller index
+  int idx = -1;
+  // a beats b: larger, or NaN over a number, or equal with the larger index
+  // (the reference's Iterator::max_by keeps the last of equal maxima)
   auto better = [](float a, int ia, float b, int ib) {
     const bool an = a != a, bn = b != b;
-    if (an || bn) return an && (!bn || ia < ib);
-    return a > b || (a == b && ia < ib);
+    if (an || bn) return an && (!bn || ia > ib);
+    return a > b || (a == b && ia > ib);
   };
   constexpr int VN = Vec16<T>::N;
   if (cols % VN == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {

@@ -21,7 +21,11 @@ MI355X-specific structure (same arithmetic):
   * prefill runs the causal FA2 kernel over the cache; each decode step runs
     teeny_decode_attention over the cached keys;
   * Linear layers (teeny-core's external `Linear`, src/layers/mod.rs:54-58,
-    y = x W^T with W [out, in]) are hipBLASLt GEMMs through torch.
+    y = x W^T with W [out, in]) are hipBLASLt GEMMs through torch for a
+    prompt; with at most 16 rows (a decode step) they are this library's
+    weight-streaming kernels: gate_up fused with SwiGLU, and q|k|v, o and
+    down split over K into fp32 slabs that the QKV split and the
+    residual-add norms sum.
 """
 from __future__ import annotations
 
@@ -99,6 +103,57 @@ def init_weights(cfg: LlamaConfig, dtype=torch.bfloat16, device="cuda", std: flo
         w[p + "mlp.gate_up_proj.weight"] = rnd(2 * F_, d)
         w[p + "mlp.down_proj.weight"] = rnd(d, F_)
     return w
+
+
+def load_hf_weights(cfg: LlamaConfig, model_dir: str, dtype=torch.bfloat16,
+                    device="cuda") -> dict:
+    """A HuggingFace Llama checkpoint (every *.safetensors file of model_dir)
+    as this model's weights (src/loader.rs:31-56): gate_proj | up_proj are
+    concatenated along rows into gate_up_proj (gate first, as the reference
+    loader does), q_proj | k_proj | v_proj likewise into qkv_proj (this
+    model's fused projection), and lm_head is the tied embedding
+    (src/llama.rs:80; an lm_head.weight in the files is not used).  Tensors
+    are read with the safetensors loader, which executes nothing from the
+    file, and converted to `dtype`."""
+    import glob
+    import os
+
+    from safetensors import safe_open
+
+    paths = sorted(glob.glob(os.path.join(model_dir, "*.safetensors")))
+    if not paths:
+        raise FileNotFoundError(f"no .safetensors files found in {model_dir}")
+    raw = {}
+    for path in paths:
+        with safe_open(path, framework="pt", device="cpu") as f:
+            for k in f.keys():
+                raw[k] = f.get_tensor(k)
+
+    def get(name, shape):
+        if name not in raw:
+            raise KeyError(f"missing weight: {name}")
+        t = raw[name]
+        if tuple(t.shape) != tuple(shape):
+            raise ValueError(f"{name}: shape {tuple(t.shape)}, the config needs {tuple(shape)}")
+        return t
+
+    d, D, Hq, Hkv, F_ = cfg.d_model, cfg.head_dim(), cfg.n_heads, cfg.n_kv_heads(), cfg.d_ff()
+    w = {"model.embed_tokens.weight": get("model.embed_tokens.weight", (cfg.vocab_size, d)),
+         "model.norm.weight": get("model.norm.weight", (d,))}
+    for i in range(cfg.n_layers):
+        p = f"model.layers.{i}."
+        a, m = p + "self_attn.", p + "mlp."
+        w[p + "input_layernorm.weight"] = get(p + "input_layernorm.weight", (d,))
+        w[p + "post_attention_layernorm.weight"] = get(p + "post_attention_layernorm.weight",
+                                                       (d,))
+        w[a + "qkv_proj.weight"] = torch.cat([get(a + "q_proj.weight", (Hq * D, d)),
+                                              get(a + "k_proj.weight", (Hkv * D, d)),
+                                              get(a + "v_proj.weight", (Hkv * D, d))], 0)
+        w[a + "o_proj.weight"] = get(a + "o_proj.weight", (d, Hq * D))
+        w[m + "gate_up_proj.weight"] = torch.cat([get(m + "gate_proj.weight", (F_, d)),
+                                                  get(m + "up_proj.weight", (F_, d))], 0)
+        w[m + "down_proj.weight"] = get(m + "down_proj.weight", (d, F_))
+    return {k: v.to(dtype).to(device).contiguous() for k, v in w.items()}
 
 
 class KVCache:
@@ -217,7 +272,7 @@ class Llama:
         cache, logits = self.prefill(prompt, prompt.shape[1] + n_new)
         out = []
         for _ in range(n_new):
-            nxt = torch.argmax(logits, dim=-1, keepdim=True)  # greedy (llama_generate.rs:252-257)
+            nxt = ops.argmax_rows(logits).view(-1, 1)  # greedy (llama_generate.rs:252-257)
             out.append(nxt)
             if len(out) == n_new:
                 break
@@ -247,7 +302,7 @@ class Llama:
             B, S = seq.shape
             cache = KVCache(self.cfg, B, S, self.w["model.norm.weight"].dtype, seq.device)
             h = self.hidden(seq, cache, 0)
-            nxt = torch.argmax(self.logits(h[:, -1]), dim=-1, keepdim=True)
+            nxt = ops.argmax_rows(self.logits(h[:, -1])).view(-1, 1)
             out.append(nxt)
             seq = torch.cat([seq, nxt], dim=1)
         return torch.cat(out, dim=1)

@@ -404,8 +404,9 @@ def decode_attention(q, k_cache, v_cache, n_keys: int, softmax_scale: float | No
 
 
 def argmax_rows(x, out=None):
-    """x [rows, cols] -> int64 [rows]: first index of each row's maximum
-    (NaN counts as the maximum), like torch.argmax(x, dim=-1)."""
+    """x [rows, cols] -> int64 [rows]: the last index of each row's maximum,
+    the reference's greedy choice (examples/llama_generate.rs:252-257,
+    Iterator::max_by); NaN counts as the maximum."""
     _dev(x)
     x2 = x.reshape(-1, x.shape[-1])
     if not x2.is_contiguous():

@@ -162,15 +162,22 @@ def test_generate_cached_equals_recompute(cuda, n_kv):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_argmax_rows(cuda, dtype):
-    """First index of the row maximum, NaN counting as the maximum (torch.argmax)."""
+    """Last index of the row maximum (the reference's Iterator::max_by), NaN
+    counting as the maximum."""
     g = torch.Generator(device="cuda").manual_seed(21)
     x = torch.randn((16, 128256), generator=g, device="cuda").to(dtype)
-    x[3, 7] = x[3, 90000] = 1e4  # tie: the first index wins
-    x[5, :] = 0.0                # all equal: index 0
+    x[3, 7] = x[3, 90000] = 1e4  # tie: the last index wins
+    x[5, :] = 0.0                # all equal: the last index
     x[9, 123] = float("nan")     # NaN is the maximum
+    x[11, :] = float("-inf")     # all -inf: the last index
     got = ops.argmax_rows(x)
-    assert torch.equal(got, torch.argmax(x, dim=-1))
-    assert got[3] == 7 and got[5] == 0 and got[9] == 123
+    n = x.shape[1]
+    # torch.argmax keeps the first maximum (and the first NaN): flip the row
+    assert torch.equal(got, n - 1 - torch.argmax(x.flip(-1), dim=-1))
+    assert got[3] == 90000 and got[5] == n - 1 and got[9] == 123 and got[11] == n - 1
+    # a row whose length is not a multiple of the vector width
+    y = x[:, :1001].contiguous()
+    assert torch.equal(ops.argmax_rows(y), 1000 - torch.argmax(y.flip(-1), dim=-1))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
