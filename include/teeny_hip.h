@@ -257,10 +257,10 @@ int teeny_argmax_rows(const void* x, int64_t* out, int rows, int cols, int dtype
 /* Decode-step linear layer y[M, N] = x[M, K] . w[N, K]^T, bf16 only, for
  * 1 <= M <= 16 (one token per sequence): replaces the external teeny-core
  * Linear behind sym_linear (src/layers/mod.rs:54-58) at the shapes a KV-cached
- * decode step has.  Requires N % 64 == 0 and K % 128 == 0; other shapes return
+ * decode step has.  Requires N % 128 == 0 and K % 128 == 0; other shapes return
  * TEENY_ERR_UNSUPPORTED (the caller then uses a general GEMM).  Deterministic.
  * teeny_linear_swiglu_bf16: w is the fused gate_up weight [2F, K] (gate rows
- * first, src/loader.rs:49-55), F % 32 == 0; writes y[M, F] =
+ * first, src/loader.rs:49-55), F % 64 == 0; writes y[M, F] =
  * silu(x w_gate^T) * (x w_up^T) with both products rounded to bf16 first, as
  * FeedForward's gate_up Linear followed by SwigluOp computes it
  * (src/layers/ffn.rs:47-56). */

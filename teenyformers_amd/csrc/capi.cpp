@@ -803,8 +803,8 @@ int teeny_argmax_rows(const void* x, int64_t* out, int rows, int cols, int dtype
   return launch(name, dim3(rows), dim3(1024), 0, stream, args);
 }
 
-// Decode-step linear layers (linear_bf16.hip): 64 W rows per workgroup
-// (32 gate + 32 up rows for SwiGLU), x staged in 512-wide K chunks.
+// Decode-step linear layers (linear_bf16.hip): 512 threads, 128 W rows per
+// workgroup (64 gate + 64 up rows for SwiGLU), x staged in 512-wide K chunks.
 static int linear_sk_check(const void* x, const void* w, const void* y, int M, int N, int K,
                            long w_rows, int row_tile) {
   if (!x || !w || !y) return TEENY_ERR_NULL_POINTER;
@@ -815,18 +815,18 @@ static int linear_sk_check(const void* x, const void* w, const void* y, int M, i
 
 int teeny_linear_bf16(const void* x, const void* w, void* y, int M, int N, int K,
                       hipStream_t stream) {
-  int rc = linear_sk_check(x, w, y, M, N, K, N, 64);
+  int rc = linear_sk_check(x, w, y, M, N, K, N, 128);
   if (rc) return rc;
   void* args[] = {&x, &w, &y, &M, &N, &K};
-  return launch("teeny_linear_sk_bf16", dim3(N / 64), dim3(256), 0, stream, args);
+  return launch("teeny_linear_sk_bf16", dim3(N / 128), dim3(512), 0, stream, args);
 }
 
 int teeny_linear_swiglu_bf16(const void* x, const void* w, void* y, int M, int F, int K,
                              hipStream_t stream) {
-  int rc = linear_sk_check(x, w, y, M, F, K, 2L * F, 32);
+  int rc = linear_sk_check(x, w, y, M, F, K, 2L * F, 64);
   if (rc) return rc;
   void* args[] = {&x, &w, &y, &M, &F, &K};
-  return launch("teeny_linear_sk_swiglu_bf16", dim3(F / 32), dim3(256), 0, stream, args);
+  return launch("teeny_linear_sk_swiglu_bf16", dim3(F / 64), dim3(512), 0, stream, args);
 }
 
 int teeny_linear_partials_count(int K, int k_split) {
@@ -837,7 +837,7 @@ int teeny_linear_partials_count(int K, int k_split) {
 
 int teeny_linear_partials_bf16(const void* x, const void* w, float* parts, int M, int N, int K,
                                int k_split, hipStream_t stream) {
-  int rc = linear_sk_check(x, w, parts, M, N, K, N, 64);
+  int rc = linear_sk_check(x, w, parts, M, N, K, N, 128);
   if (rc) return rc;
   if (k_split <= 0) return TEENY_ERR_INVALID_VALUE;
   if (k_split >= K) k_split = K;
@@ -845,7 +845,7 @@ int teeny_linear_partials_bf16(const void* x, const void* w, float* parts, int M
   const int n = teeny_linear_partials_count(K, k_split);
   if (n > 65535) return TEENY_ERR_INVALID_SHAPE;
   void* args[] = {&x, &w, &parts, &M, &N, &K, &k_split};
-  return launch("teeny_linear_sk_part_bf16", dim3(N / 64, n), dim3(256), 0, stream, args);
+  return launch("teeny_linear_sk_part_bf16", dim3(N / 128, n), dim3(512), 0, stream, args);
 }
 
 int teeny_token_embed_fwd(const void* ids, const void* weight, void* out, int seq_len,

@@ -6,10 +6,10 @@
 // (src/loader.rs:19-27).  With M <= 16 the product is bound by streaming W
 // from HBM once.
 //
-// A workgroup of 4 wavefronts owns 64 output features (16 W rows per
+// A workgroup of 8 wavefronts owns 128 output features (16 W rows per
 // wavefront) and one K range.  x is staged in LDS in 512-wide K chunks,
-// double-buffered and shared by the four wavefronts, so the L2 -> CU traffic
-// for x is a quarter of W's (reading x from L2 once per 16 rows capped the W
+// double-buffered and shared by the eight wavefronts, so the L2 -> CU traffic
+// for x is an eighth of W's (reading x from L2 once per 16 rows capped the W
 // stream near 4 TB/s).  A wavefront loads the four 128-wide K steps of a
 // chunk for its 16 rows into registers (lane (r = lane % 16, g = lane / 16):
 // 64 contiguous bytes of row r at k = 128 j + 32 g), then issues
@@ -18,7 +18,7 @@
 //
 // Outputs:
 //   teeny_linear_sk_bf16        one K range (K), y bf16 [M, N]
-//   teeny_linear_sk_swiglu_bf16 wavefronts 0-1 compute gate rows, 2-3 the
+//   teeny_linear_sk_swiglu_bf16 wavefronts 0-3 compute gate rows, 4-7 the
 //                               matching up rows of the fused gate_up weight;
 //                               y [M, F] = silu(gate) * up, both rounded to
 //                               bf16 first as the unfused path stores them
@@ -32,6 +32,7 @@
 
 namespace {
 
+constexpr int NW = 8;            // wavefronts per workgroup
 constexpr int XC = 512;          // K per staged x chunk (4 steps of 128)
 constexpr int XS = XC * 2 + 16;  // bytes per LDS x row; the pad spreads rows over banks
 
@@ -53,26 +54,30 @@ __device__ void linear_sk(const bf16* __restrict__ x, const bf16* __restrict__ w
   // first W row of this wavefront
   int row0;
   if constexpr (MODE == SK_SWIGLU)
-    row0 = blockIdx.x * 32 + 16 * (wave & 1) + (wave >> 1) * N;  // N = F: up rows follow
+    row0 = blockIdx.x * (8 * NW) + 16 * (wave % (NW / 2)) + (wave / (NW / 2)) * N;  // N = F
   else
-    row0 = blockIdx.x * 64 + 16 * wave;
+    row0 = blockIdx.x * (16 * NW) + 16 * wave;
   const int kb = blockIdx.y * KC, ke = min(kb + KC, K);
   const int nch = (ke - kb + XC - 1) / XC;
   const bf16* wr = w + (long)(row0 + r) * K + 32 * g;
 
-  // x staging: thread t copies 16-byte pieces (t % 16) + 16 j of row t / 16
-  const int xm = tid >> 4, xp = tid & 15;
+  // x staging: a chunk row is 64 16-byte pieces (16 per 128-wide step);
+  // thread t copies pieces P = t % TP + TP j of row t / TP
+  constexpr int TP = NW * 64 / 16, XJ = 64 / TP;
+  const int xm = tid / TP, xp = tid % TP;
   const bf16* xsrc = x + (long)min(xm, M - 1) * K + 8 * xp;
-  u32x4 xv[4];
+  u32x4 xv[XJ];
   auto xload = [&](int k0, int nsteps) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (j < nsteps) xv[j] = *reinterpret_cast<const u32x4*>(xsrc + k0 + 128 * j);
+    for (int j = 0; j < XJ; ++j)
+      if ((xp + TP * j) / 16 < nsteps)
+        xv[j] = *reinterpret_cast<const u32x4*>(xsrc + k0 + 8 * TP * j);
   };
   auto xstore = [&](int buf, int nsteps) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (j < nsteps) *reinterpret_cast<u32x4*>(xs[buf] + xm * XS + 16 * (xp + 16 * j)) = xv[j];
+    for (int j = 0; j < XJ; ++j)
+      if ((xp + TP * j) / 16 < nsteps)
+        *reinterpret_cast<u32x4*>(xs[buf] + xm * XS + 16 * (xp + TP * j)) = xv[j];
   };
   auto steps_of = [&](int k0) { return min(4, (ke - k0) >> 7); };
 
@@ -114,9 +119,9 @@ __device__ void linear_sk(const bf16* __restrict__ x, const bf16* __restrict__ w
   if constexpr (MODE == SK_SWIGLU) {
     __syncthreads();  // done with xs: reuse it for the up halves
     f32x4* up = reinterpret_cast<f32x4*>(xs[0]);
-    if (wave >= 2) up[(wave - 2) * 64 + lane] = acc;
+    if (wave >= NW / 2) up[(wave - NW / 2) * 64 + lane] = acc;
     __syncthreads();
-    if (wave < 2 && r < M) {
+    if (wave < NW / 2 && r < M) {
       const f32x4 u = up[wave * 64 + lane];
       float o[4];
 #pragma unroll
@@ -124,7 +129,7 @@ __device__ void linear_sk(const bf16* __restrict__ x, const bf16* __restrict__ w
         const float gate = (float)(bf16)acc[i], upv = (float)(bf16)u[i];
         o[i] = gate * (1.0f / (1.0f + expf(-gate))) * upv;
       }
-      bf16* y = (bf16*)out + (long)r * N + blockIdx.x * 32 + 16 * wave + 4 * g;
+      bf16* y = (bf16*)out + (long)r * N + blockIdx.x * (8 * NW) + 16 * wave + 4 * g;
       *reinterpret_cast<u32x2*>(y) = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
     }
   } else if (r < M) {
@@ -141,17 +146,17 @@ __device__ void linear_sk(const bf16* __restrict__ x, const bf16* __restrict__ w
 
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256) void teeny_linear_sk_bf16(
+extern "C" __global__ __launch_bounds__(NW * 64) void teeny_linear_sk_bf16(
     const bf16* x, const bf16* w, bf16* y, int M, int N, int K) {
   linear_sk<SK_BF16>(x, w, y, M, N, K, K);
 }
 
-extern "C" __global__ __launch_bounds__(256) void teeny_linear_sk_swiglu_bf16(
+extern "C" __global__ __launch_bounds__(NW * 64) void teeny_linear_sk_swiglu_bf16(
     const bf16* x, const bf16* w, bf16* y, int M, int F, int K) {
   linear_sk<SK_SWIGLU>(x, w, y, M, F, K, K);
 }
 
-extern "C" __global__ __launch_bounds__(256) void teeny_linear_sk_part_bf16(
+extern "C" __global__ __launch_bounds__(NW * 64) void teeny_linear_sk_part_bf16(
     const bf16* x, const bf16* w, float* part, int M, int N, int K, int KC) {
   linear_sk<SK_PART>(x, w, part, M, N, K, KC);
 }

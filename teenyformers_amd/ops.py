@@ -417,7 +417,7 @@ def argmax_rows(x, out=None):
     return out
 
 
-def _skinny(x2: torch.Tensor, w: torch.Tensor, n_out: int, row_tile: int = 64) -> bool:
+def _skinny(x2: torch.Tensor, w: torch.Tensor, n_out: int, row_tile: int = 128) -> bool:
     """Shapes the decode-step linear kernels take (else a general GEMM runs)."""
     M, K = x2.shape
     if torch.is_grad_enabled() and (x2.requires_grad or w.requires_grad):
@@ -450,7 +450,7 @@ def linear_swiglu(x: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
     if K != x2.shape[1] or N2 % 2:
         raise ValueError("linear_swiglu: weight must be [2F, in] with in = x's features")
     F = N2 // 2
-    if not _skinny(x2, w_gate_up, F, row_tile=32):
+    if not _skinny(x2, w_gate_up, F, row_tile=64):
         return swiglu(torch.nn.functional.linear(x, w_gate_up))
     x2 = x2.contiguous()
     y = torch.empty((x2.shape[0], F), dtype=x.dtype, device=x.device)
@@ -475,13 +475,12 @@ class Partials:
         return self.slabs.sum(0, dtype=torch.float32).to(self.dtype).view(self.shape)
 
 
-def _k_split(N: int, K: int) -> int:
-    """K per slab: about 384 workgroups of 64 features in all (each slab costs
-    the consumer a read), 512-wide chunks."""
-    groups = N // 64
-    splits = max(1, min(K // 512, -(-384 // groups)))
-    per = -(-K // splits)
-    return -(-per // 512) * 512
+def _k_split(K: int, N: int) -> int:
+    """K per slab, in whole 512-wide chunks: enough slabs that the 128-feature
+    workgroups fill the GPU (about 256), at most 8 (each slab costs the
+    consumer a read)."""
+    splits = min(8, max(-(-256 // (N // 128)), -(-K // (7 * 512))))
+    return max(512, -(-K // (splits * 512)) * 512)
 
 
 def linear_split(x: torch.Tensor, w: torch.Tensor):
@@ -494,7 +493,7 @@ def linear_split(x: torch.Tensor, w: torch.Tensor):
     if not _skinny(x2, w, N):
         return torch.nn.functional.linear(x, w)
     x2 = x2.contiguous()
-    ks = _k_split(N, K) if K >= 1024 else K
+    ks = _k_split(K, N)
     n = _lib.lib().teeny_linear_partials_count(K, ks)
     slabs = torch.empty((n, x2.shape[0], N), dtype=torch.float32, device=x.device)
     call("teeny_linear_partials_bf16", _p(x2), _p(w), _p(slabs), x2.shape[0], N, K, ks,

