@@ -61,6 +61,8 @@ def main() -> int:
                     help="skip the long-context GQA, Llama block and Llama-8B measurements")
     ap.add_argument("--no-power", action="store_true",
                     help="skip the power / clock sampling phase")
+    ap.add_argument("--bandwidth-only", action="store_true",
+                    help="only the HBM-bound kernels at the Llama-block shapes (one JSON line)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed steps, run one head transpose (a pure copy) of "
                          "Q's 256 MiB, the known-size reference for HBM byte counters")
@@ -78,6 +80,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     _lib.lib()
+    if args.bandwidth_only:
+        print(json.dumps({"bandwidth_c2": bench_bandwidth(torch, ops, _lib)}), flush=True)
+        return 0
     gen = torch.Generator(device=dev).manual_seed(1234)
     shape = (B, H, S, D)
     q, k, v, do = (torch.randn(shape, generator=gen, device=dev).to(torch.bfloat16)
@@ -173,6 +178,7 @@ def main() -> int:
     if not args.no_extra:
         del q, k, v, do, o, lse, dq, dk, dv, ws
         torch.cuda.empty_cache()
+        out["detail"]["bandwidth_c2"] = bench_bandwidth(torch, ops, _lib)
         out["detail"]["fa2_gqa_long"] = bench_gqa_long(torch, ops)
         out["detail"]["llama_block"] = bench_llama_block(torch)
         out["detail"]["llama_8b_shape"] = bench_llama_8b(torch)
@@ -222,6 +228,71 @@ def bench_gqa_long(torch, ops):
                          "fwd_pct_peak": round(f / fwd_ms / 1e9 / PEAK_BF16_TFLOPS, 4),
                          "bwd_pct_peak": round(2.5 * f / bwd_ms / 1e9 / PEAK_BF16_TFLOPS, 4)}
         del q, k, v, do, o, lse
+    return res
+
+
+def bench_bandwidth(torch, ops, lib, reps: int = 20):
+    """The HBM-bound kernels at the Llama-block shapes (B4 S2048, d2048, Hq32
+    Hkv8 D64, F8192, bf16): RoPE, head transposes, RMSNorm, residual-add
+    RMSNorm, SwiGLU.  Duration per call = HIP events (on the launch stream)
+    around one replay of a graph of `reps` calls, / reps; bytes are the
+    algorithmic reads + writes.  A torch device copy of Q's bytes is the
+    size's practical ceiling."""
+    B, S, Hq, Hkv, D, dm, F = 4, 2048, 32, 8, 64, 2048, 8192
+    M = B * S
+    gen = torch.Generator(device="cuda").manual_seed(7)
+
+    def rnd(*shape):
+        return torch.randn(shape, generator=gen, device="cuda").to(torch.bfloat16)
+
+    q, k = rnd(B * Hq, S, D), rnd(B * Hkv, S, D)
+    xq = rnd(B, S, Hq * D)
+    x, r, w = rnd(M, dm), rnd(M, dm), rnd(dm)
+    z = rnd(M, 2 * F)
+    qo, ko = torch.empty_like(q), torch.empty_like(k)
+    cases = [
+        ("rope_fwd Q [128,2048,64]", lambda: ops.rope(q, 5e5, out=qo), 2 * q.numel() * 2),
+        ("rope_fwd K [32,2048,64]", lambda: ops.rope(k, 5e5, out=ko), 2 * k.numel() * 2),
+        ("transpose_heads Q [4,2048,32*64]", lambda: ops.transpose_heads(xq, Hq),
+         2 * xq.numel() * 2),
+        ("merge_heads O [4,32,2048,64]", lambda: ops.merge_heads(qo.view(B, Hq, S, D)),
+         2 * qo.numel() * 2),
+        ("rmsnorm [8192,2048]", lambda: ops.rmsnorm(x, w, 1e-5), 2 * M * dm * 2 + dm * 2 + M * 4),
+        ("fused_add_rmsnorm [8192,2048]", lambda: ops.fused_add_rmsnorm(x, r, w, 1e-5),
+         4 * M * dm * 2 + dm * 2 + M * 4),
+        ("swiglu_fwd [8192,2*8192]", lambda: ops.swiglu(z), 3 * M * F * 2),
+    ]
+    qc = torch.empty_like(q)
+    cases.append(("torch copy of Q's bytes (reference)", lambda: qc.copy_(q), 2 * q.numel() * 2))
+    res = {}
+    for name, fn, nbytes in cases:
+        lib.profile_enable(True)  # one call recorded: which kernels it launches
+        fn()
+        torch.cuda.synchronize()
+        lib.profile_enable(False)
+        kernels = sorted(lib.profile_stats())
+        # reps calls captured in one HIP graph, so the host's launch cost
+        # (comparable to these ~10 us kernels) does not starve the GPU
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        graph.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        del graph
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "gbs": round(gbs, 1),
+                     "pct_hbm_peak": round(gbs / PEAK_HBM_GBS, 4), "kernels": kernels}
     return res
 
 

@@ -447,13 +447,17 @@ static int rope_impl(const void* x, void* y, int n_ctx, float ln_base, int bh, i
   if (n_ctx <= 0 || bh <= 0 || head_dim <= 0 || (long)bh * n_ctx * head_dim >= kMaxElems)
     return TEENY_ERR_INVALID_SHAPE;
   const int vn = dtype == TEENY_BF16 ? 8 : 4;
-  if (head_dim % vn != 0) return TEENY_ERR_UNSUPPORTED;
+  // D a power of two, as the reference requires (src/kernels/rope.rs:56)
+  if (head_dim % vn != 0 || (head_dim & (head_dim - 1)) != 0) return TEENY_ERR_UNSUPPORTED;
   if (!std::isfinite(ln_base)) return TEENY_ERR_INVALID_VALUE;
   char name[32];
   snprintf(name, sizeof name, "teeny_rope_%s", dtype_tag(dtype));
   void* args[] = {&x, &y, &bh, &n_ctx, &head_dim, &ln_base, &backward};
-  unsigned shmem = 16u * (unsigned)(head_dim / 2) * 8u;
-  return launch(name, dim3((n_ctx + 15) / 16, (bh + 15) / 16), dim3(256), shmem, stream, args);
+  // a thread per (position, 16-byte vector) of 8 rows; head_dim / vn vectors per row
+  const int ppw = 256 / (head_dim / vn);  // positions per workgroup
+  if (ppw < 1) return TEENY_ERR_UNSUPPORTED;
+  if ((bh + 7) / 8 > 65535) return TEENY_ERR_INVALID_SHAPE;
+  return launch(name, dim3((n_ctx + ppw - 1) / ppw, (bh + 7) / 8), dim3(256), 0, stream, args);
 }
 
 int teeny_rope_fwd(const void* x, void* y, int n_ctx, float ln_rope_base, int bh, int head_dim,

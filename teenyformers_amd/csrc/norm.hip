@@ -74,6 +74,17 @@ __device__ void rmsnorm_fwd_row(const T* __restrict__ x, const T* __restrict__ r
       }
     }
   }
+  // up to 4 chunks the weights are read with the row, not after the
+  // reduction (wider rows would double the registers of a wavefront)
+  constexpr bool kPre = CH <= 4;
+  float wv[kPre ? CH : 1][VEC];
+  if constexpr (kPre) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      int idx = (c * 64 + lane) * VEC;
+      if (idx < N) ldv<T, VEC>(w + idx, wv[c]);
+    }
+  }
   sq = wave_sum(sq);
   const float rs = 1.0f / sqrtf(sq * (1.0f / (float)N) + eps);
   if (lane == 0 && rstd) rstd[row] = rs;
@@ -81,10 +92,11 @@ __device__ void rmsnorm_fwd_row(const T* __restrict__ x, const T* __restrict__ r
   for (int c = 0; c < CH; ++c) {
     int idx = (c * 64 + lane) * VEC;
     if (idx < N) {
-      float wv[VEC], out[VEC];
-      ldv<T, VEC>(w + idx, wv);
+      float out[VEC];
+      float* wc = wv[kPre ? c : 0];
+      if constexpr (!kPre) ldv<T, VEC>(w + idx, wc);
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) out[j] = hv[c][j] * rs * wv[j];
+      for (int j = 0; j < VEC; ++j) out[j] = hv[c][j] * rs * wc[j];
       stv<T, VEC>(y + base + idx, out);
     }
   }
@@ -224,6 +236,12 @@ __device__ void rmsnorm_fwd_row_wg(const T* __restrict__ x, const T* __restrict_
       }
     }
   }
+  float wv[CH][VEC];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    int idx = (c * 256 + tid) * VEC;
+    if (idx < N) ldv<T, VEC>(w + idx, wv[c]);
+  }
   sq = wave_sum(sq);
   if ((tid & 63) == 0) part[tid >> 6] = sq;
   __syncthreads();
@@ -234,10 +252,9 @@ __device__ void rmsnorm_fwd_row_wg(const T* __restrict__ x, const T* __restrict_
   for (int c = 0; c < CH; ++c) {
     int idx = (c * 256 + tid) * VEC;
     if (idx < N) {
-      float wv[VEC], out[VEC];
-      ldv<T, VEC>(w + idx, wv);
+      float out[VEC];
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) out[j] = hv[c][j] * rs * wv[j];
+      for (int j = 0; j < VEC; ++j) out[j] = hv[c][j] * rs * wv[c][j];
       stv<T, VEC>(y + base + idx, out);
     }
   }

@@ -2,11 +2,13 @@
 //
 // Reference: rope_forward / rope_backward (src/kernels/rope.rs:57-140), one
 // 128-thread CTA per (position, bh) row that recomputes exp, cos and sin for
-// every pair of every row.  Here a workgroup owns kPos positions x kHeads
-// rows of BH: it first evaluates the (cos, sin) table for its kPos positions
-// into LDS once, then streams kHeads * kPos rows through 16-byte vectors, so
-// the transcendental work is amortised over kHeads rows and the kernel is
-// HBM bound.
+// every pair of every row.  Here a thread owns one 16-byte vector column
+// (position s, pairs v*VN/2 ..) of kHeads consecutive BH rows: it issues the
+// kHeads loads first, evaluates its VN/2 (cos, sin) pairs while they are in
+// flight, and rotates and stores the kHeads vectors, so the transcendental
+// work is amortised over kHeads rows, no LDS table or barrier is needed, and
+// the kernel is HBM bound.  (A workgroup-shared LDS table for 16 positions x
+// 16 rows ran at 3.8 TB/s at [128, 2048, 64] bf16, this layout at 5.3.)
 //
 // theta parity with the oracle: inv_freq[k] = fp32(exp_f64(fp32(k) * c)) with
 // c = (-2 * ln_base) / HEAD_DIM in fp32 (rope.rs:88), theta = fp32(pos) *
@@ -16,50 +18,47 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kPos = 16;    // positions per workgroup
-constexpr int kHeads = 16;  // BH rows per position per workgroup
+constexpr int kHeads = 8;  // BH rows per thread
 
+// grid: (ceil(n_ctx / (kThreads / vpr)), ceil(bh / kHeads)); head_dim is a
+// power of two (vpr = head_dim / VN vectors per row).
 template <typename T>
 __device__ void rope_rows(const T* __restrict__ x, T* __restrict__ y, int bh_total, int n_ctx,
                           int head_dim, float ln_base, int backward) {
-  extern __shared__ float2 cs_tab[];  // [kPos][head_dim / 2] (cos, sin)
-  const int half = head_dim / 2;
-  const int s0 = blockIdx.x * kPos;
-  const int bh0 = blockIdx.y * kHeads;
-  const float c = (-2.0f * ln_base) / (float)head_dim;
-  for (int i = threadIdx.x; i < kPos * half; i += kThreads) {
-    int p = i / half, k = i - p * half;
-    float inv = (float)exp((double)((float)k * c));
-    float theta = (float)(s0 + p) * inv;
-    float sn, cn;
-    sincosf(theta, &sn, &cn);
-    cs_tab[i] = make_float2(cn, sn);
-  }
-  __syncthreads();
-
   constexpr int VN = Vec16<T>::N;  // elements per 16-byte vector (even)
-  const int vpr = head_dim / VN;   // vectors per row
-  const int total = kHeads * kPos * vpr;
-  const float sgn = backward ? -1.0f : 1.0f;
-  for (int i = threadIdx.x; i < total; i += kThreads) {
-    int v = i % vpr;
-    int r = i / vpr;
-    int p = r % kPos;
-    int hh = r / kPos;
-    int s = s0 + p, bh = bh0 + hh;
-    if (s >= n_ctx || bh >= bh_total) continue;
-    long off = ((long)bh * n_ctx + s) * head_dim + v * VN;
-    float in[VN], out[VN];
-    Vec16<T>::load(x + off, in);
-    const float2* cs = cs_tab + p * half + v * (VN / 2);
+  const int vpr = head_dim / VN;
+  const int lg_vpr = __builtin_ctz(vpr);
+  const int v = threadIdx.x & (vpr - 1);
+  const int s = blockIdx.x * (kThreads >> lg_vpr) + (threadIdx.x >> lg_vpr);
+  const int bh0 = blockIdx.y * kHeads;
+  if (s >= n_ctx) return;
+  const long off0 = ((long)bh0 * n_ctx + s) * head_dim + v * VN;
+  const long hstride = (long)n_ctx * head_dim;
+  float in[kHeads][VN];
+#pragma unroll
+  for (int h = 0; h < kHeads; ++h)
+    if (bh0 + h < bh_total) Vec16<T>::load(x + off0 + h * hstride, in[h]);
+
+  const float c = (-2.0f * ln_base) / (float)head_dim;
+  float cn[VN / 2], sn[VN / 2];
+#pragma unroll
+  for (int j = 0; j < VN / 2; ++j) {
+    const int k = v * (VN / 2) + j;
+    const float inv = (float)exp((double)((float)k * c));
+    sincosf((float)s * inv, &sn[j], &cn[j]);
+    if (backward) sn[j] = -sn[j];
+  }
+#pragma unroll
+  for (int h = 0; h < kHeads; ++h) {
+    if (bh0 + h >= bh_total) continue;
+    float out[VN];
 #pragma unroll
     for (int j = 0; j < VN / 2; ++j) {
-      float cn = cs[j].x, sn = sgn * cs[j].y;
-      float x0 = in[2 * j], x1 = in[2 * j + 1];
-      out[2 * j] = x0 * cn - x1 * sn;
-      out[2 * j + 1] = x0 * sn + x1 * cn;
+      const float x0 = in[h][2 * j], x1 = in[h][2 * j + 1];
+      out[2 * j] = x0 * cn[j] - x1 * sn[j];
+      out[2 * j + 1] = x0 * sn[j] + x1 * cn[j];
     }
-    Vec16<T>::store(y + off, out);
+    Vec16<T>::store(y + off0 + h * hstride, out);
   }
 }
 

@@ -69,6 +69,7 @@ def test_fa2_bwd_workspace(L):
 def test_other_ops_validation(L):
     assert L.teeny_rope_fwd(P, P, 8, 9.21, 2, 12, BF16, None) == UNSUP  # 12 % 8
     assert L.teeny_rope_fwd(None, P, 8, 9.21, 2, 16, F32, None) == NULLP
+    assert L.teeny_rope_fwd(P, P, 8, 9.21, 2, 24, F32, None) == UNSUP  # not a power of two
     assert L.teeny_transpose_heads(P, P, 0, 4, 1, 64, BF16, None) == SHAPE
     assert L.teeny_transpose_heads(P, P, 8, 4, 1, 64, BF16, None) == VALUE  # src == dst
     assert L.teeny_rmsnorm_fwd(P, P, None, P, 4, 64 * 8 * 32, 1e-5, BF16, None) == UNSUP
@@ -76,3 +77,28 @@ def test_other_ops_validation(L):
     assert L.teeny_fused_add_rmsnorm_bwd(P, P, P, P, P, P, P, 4, 16, F32, None, 0, None) == WS
     assert L.teeny_swiglu_fwd(P, P, 0, 8, F32, None) == SHAPE
     assert L.teeny_token_embed_fwd(P, P, P, 4, 16, 10, BF16, F32, None) == UNSUP  # ids dtype
+
+
+def test_decode_ops_validation(L):
+    # decode-step linears: M <= 16, N % 128 (F % 64), K % 128
+    assert L.teeny_linear_bf16(P, P, P, 17, 128, 128, None) == UNSUP
+    assert L.teeny_linear_bf16(P, P, P, 16, 64, 128, None) == UNSUP
+    assert L.teeny_linear_bf16(P, P, P, 16, 128, 96, None) == UNSUP
+    assert L.teeny_linear_bf16(None, P, P, 16, 128, 128, None) == NULLP
+    assert L.teeny_linear_bf16(P, P, P, 0, 128, 128, None) == SHAPE
+    assert L.teeny_linear_swiglu_bf16(P, P, P, 4, 32, 128, None) == UNSUP
+    assert L.teeny_linear_partials_bf16(P, P, P, 4, 128, 4096, 1000, None) == VALUE
+    assert L.teeny_linear_partials_bf16(P, P, P, 4, 128, 4096, 0, None) == VALUE
+    assert L.teeny_linear_partials_count(4096, 1024) == 4
+    assert L.teeny_linear_partials_count(14336, 2048) == 7
+    assert L.teeny_linear_partials_count(4096, 8192) == 1
+    assert L.teeny_fused_add_rmsnorm_partials_fwd(P, 0, P, P, P, P, P, 4, 1024, 1e-5, BF16,
+                                                  None) == SHAPE
+    assert L.teeny_fused_add_rmsnorm_partials_fwd(None, 2, P, P, P, P, P, 4, 1024, 1e-5, BF16,
+                                                  None) == NULLP
+    assert L.teeny_qkv_rope_split_partials_dev(P, 2, P, P, P, 4, 1, None, 64, 8, 2, 64,
+                                               9.21, BF16, None) == NULLP
+    assert L.teeny_qkv_rope_split_partials_dev(P, 2, P, P, P, 4, 1, P, 64, 8, 3, 64,
+                                               9.21, BF16, None) == SHAPE  # 8 % 3
+    assert L.teeny_argmax_rows(None, P, 4, 10, BF16, None) == NULLP
+    assert L.teeny_argmax_rows(P, P, 0, 10, BF16, None) == SHAPE
