@@ -261,32 +261,26 @@ int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void
   char name[64];
   if (dtype == TEENY_BF16) {
     float* ld = (float*)workspace;
-    const long prows = (long)batch * hq * ((n_ctx_q + kLdRows - 1) / kLdRows * kLdRows);
-    const int rows_per_block = 256 / (head_dim / 8);
-    snprintf(name, sizeof name, "teeny_fa2_bwd_pre_bf16_d%d", head_dim);
-    void* a0[] = {&o, &dout, &l, &ld, &n_ctx_q, (void*)&prows};
-    rc = launch(name, dim3((unsigned)((prows + rows_per_block - 1) / rows_per_block)), dim3(256),
-                0, stream, a0);
+    // dQ first: one workgroup per 128 query rows of a (b, q head); it also
+    // writes LSE * log2(e) and Delta of its rows to ld for the dK/dV kernel
+    int nmb = (n_ctx_q + 127) / 128;
+    long total = (long)nmb * batch * hq;
+    if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
+    int tot = (int)total;
+    snprintf(name, sizeof name, "teeny_fa2_bwd_dq_bf16_d%d_%s", head_dim, cz);
+    void* a2[] = {&q,       &k,       &v,     &o,  &dout, &l,   &ld,  &dq,
+                  &n_ctx_q, &n_ctx_k, &scale, &hq, &hkv,  &nmb, &tot};
+    rc = launch(name, dim3(tot), dim3(256), 0, stream, a2);
     if (rc) return rc;
     // dK, dV: one workgroup per 128 keys of a (b, kv head)
     int nnb = (n_ctx_k + 127) / 128;
-    long total = (long)nnb * batch * hkv;
+    total = (long)nnb * batch * hkv;
     if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
-    int tot = (int)total;
+    tot = (int)total;
     snprintf(name, sizeof name, "teeny_fa2_bwd_dkdv_bf16_d%d_%s", head_dim, cz);
     void* a1[] = {&q,       &k,       &v,     &dout, &ld,  &dk,  &dv,
                   &n_ctx_q, &n_ctx_k, &scale, &hq,   &hkv, &nnb, &tot};
-    rc = launch(name, dim3(tot), dim3(256), 0, stream, a1);
-    if (rc) return rc;
-    // dQ: one workgroup per 128 query rows of a (b, q head)
-    int nmb = (n_ctx_q + 127) / 128;
-    total = (long)nmb * batch * hq;
-    if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
-    tot = (int)total;
-    snprintf(name, sizeof name, "teeny_fa2_bwd_dq_bf16_d%d_%s", head_dim, cz);
-    void* a2[] = {&q,     &k,   &v,   &dout, &ld,  &dq, &n_ctx_q,
-                  &n_ctx_k, &scale, &hq, &hkv, &nmb, &tot};
-    return launch(name, dim3(tot), dim3(256), 0, stream, a2);
+    return launch(name, dim3(tot), dim3(256), 0, stream, a1);
   }
   snprintf(name, sizeof name, "teeny_fa2_bwd_pre_f32_d%d", head_dim);
   void* a0[] = {&o, &dout, &delta, (void*)&rows};

@@ -6,11 +6,15 @@
 //   dS = P o (dP - Delta) with Delta = rowsum(O o dO), dQ = scale dS K,
 //   dK = scale dS^T Q.
 // The reference runs one CTA per query row and adds dK/dV with fp32 atomics
-// (nondeterministic).  Here the backward is three kernels, all deterministic
-// and free of atomics:
-//   1. bwd_pre: per block of 32 query rows, LSE * log2(e) and
-//      Delta = rowsum(O o dO) in fp32 (rows past nq: +inf and 0, so the
-//      padded rows contribute P = 0);
+// (nondeterministic).  Here the backward is two kernels, both deterministic
+// and free of atomics, launched dQ first:
+//   1. dQ, query-parallel, shaped like the forward: each wave's Q and dO
+//      rows are B operands in registers, 64-key tiles of K and V stream
+//      through LDS (K^T via the transpose read), S^T and dP^T put one query
+//      row in each lane, and dQ^T += K^T dS^T accumulates in registers.  Its
+//      prologue forms Delta = rowsum(O o dO) for its rows in fp32 and writes
+//      LSE * log2(e) and Delta per block of 32 rows for the next kernel (rows
+//      past nq: +inf and 0, so the padded rows contribute P = 0);
 //   2. dK/dV, key-parallel: one workgroup (4 wavefronts) owns 128 keys of one
 //      (b, kv head); each wave's 32 K rows stay in registers and the block's
 //      V rows in LDS as B operands of v_mfma_f32_32x32x16_bf16, and it walks
@@ -18,11 +22,7 @@
 //      streamed into double-buffered LDS by buffer_load ... lds and read both
 //      row-wise and, through the LDS transpose read, as Q^T / dO^T),
 //      accumulating dK^T and dV^T in registers: the GQA reduction comes for
-//      free;
-//   3. dQ, query-parallel, shaped like the forward: each wave's Q and dO
-//      rows are B operands in registers, 64-key tiles of K and V stream
-//      through LDS (K^T via the transpose read), S^T and dP^T put one query
-//      row in each lane, and dQ^T += K^T dS^T accumulates in registers.
+//      free.
 // Recomputing S and dP in the dQ kernel costs 7 matrix products per tile
 // pair instead of 5; in exchange neither kernel needs dS round trips through
 // LDS, fp32 atomics or a dQ accumulator in HBM.
@@ -39,35 +39,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // Per (b, q head) and block of BM query rows, ld holds BM values of
 // LSE * log2(e) followed by BM values of Delta = rowsum(O o dO), fp32; rows
-// past nq hold +inf and 0.  One thread group of D/8 lanes per (padded) row.
-template <int D>
-__device__ void bwd_pre(const bf16* __restrict__ o, const bf16* __restrict__ dout,
-                        const float* __restrict__ lse, float* __restrict__ ld, int nq,
-                        long padded_rows) {
-  constexpr int TPR = D / 8;  // threads per row, 8 elements each
-  const long prow = (long)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
-  const int c = threadIdx.x % TPR;
-  const int nq_pad = (nq + BM - 1) / BM * BM;
-  const long bh = prow / nq_pad;
-  const int i = (int)(prow - bh * nq_pad);
-  const bool ok = prow < padded_rows && i < nq;
-  float s = 0.0f;
-  if (ok) {
-    const long row = bh * nq + i;
-    float a[8], bb[8];
-    Vec16<bf16>::load(o + row * D + 8 * c, a);
-    Vec16<bf16>::load(dout + row * D + 8 * c, bb);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) s += a[j] * bb[j];
-  }
-#pragma unroll
-  for (int off = TPR / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-  if (prow < padded_rows && c == 0) {
-    float* blk = ld + (prow / BM) * (2 * BM);
-    blk[i % BM] = ok ? lse[bh * nq + i] * kLog2e : INFINITY;
-    blk[BM + i % BM] = ok ? s : 0.0f;
-  }
-}
+// past nq hold +inf and 0.  The dQ kernel writes it, the dK/dV kernel reads it.
 
 // ===========================================================================
 // dK / dV (key-parallel)
@@ -354,8 +326,9 @@ struct __attribute__((aligned(16))) DqSmem {
 
 template <int D, bool CAUSAL>
 __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ k,
-                           const bf16* __restrict__ v, const bf16* __restrict__ dout,
-                           const float* __restrict__ ld, bf16* __restrict__ dq, int nq, int nk,
+                           const bf16* __restrict__ v, const bf16* __restrict__ o,
+                           const bf16* __restrict__ dout, const float* __restrict__ lse,
+                           float* __restrict__ ld, bf16* __restrict__ dq, int nq, int nk,
                            float scale, int hq, int hkv, int num_m_blocks, int total_blocks) {
   constexpr int DC = D / 16;
   constexpr int DT = D / 32;
@@ -395,11 +368,40 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
       doreg[c] = as_bf16x8(*reinterpret_cast<const u32x4*>(dp + 16 * c));
     }
   }
-  // LSE * log2(e) and Delta of this row (rows past nq: +inf and 0)
-  const int nq_pad = (nq + BM - 1) / BM * BM;
-  const float* ldr = ld + ((long)bh * nq_pad + min(qrow, nq_pad - 1)) / BM * (2 * BM);
-  const float lse2 = qok ? ldr[qrow % BM] : INFINITY;
-  const float dlt = qok ? ldr[BM + qrow % BM] : 0.0f;
+  // LSE * log2(e) and Delta = rowsum(O o dO) of this row (rows past nq: +inf
+  // and 0): the lane holds half of the row's d values (8 g + 16 c ..), the
+  // other half is in lane l ^ 32.  Written to ld for the dK/dV kernel, which
+  // runs after this one.
+  float lse2 = INFINITY, dlt = 0.0f;
+  {
+    const long row = (long)bh * nq + min(qrow, nq - 1);
+    const bf16* op = o + row * D + 8 * g;
+    float part = 0.0f;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      float a[8], bb[8];
+      Vec16<bf16>::load(op + 16 * c, a);
+      const u32x4 dw = __builtin_bit_cast(u32x4, doreg[c]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bb[2 * j] = bf16lo(dw[j]);
+        bb[2 * j + 1] = bf16hi(dw[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) part += a[j] * bb[j];
+    }
+    part += other_half(part);
+    if (qok) {
+      lse2 = lse[(long)bh * nq + qrow] * kLog2e;
+      dlt = part;
+    }
+    const int nq_pad = (nq + BM - 1) / BM * BM;  // ld rows: whole blocks of BM
+    if (g == 0 && qrow < nq_pad) {
+      float* blk = ld + ((long)bh * nq_pad + qrow) / BM * (2 * BM);
+      blk[qrow % BM] = lse2;
+      blk[BM + qrow % BM] = dlt;
+    }
+  }
   const float sl2 = scale * kLog2e;
 
   int kend = nk;
@@ -588,10 +590,6 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
 }  // namespace
 
 #define TEENY_FA2_BWD_BF16_INST(D)                                                              \
-  extern "C" __global__ __launch_bounds__(256) void teeny_fa2_bwd_pre_bf16_d##D(               \
-      const bf16* o, const bf16* dout, const float* lse, float* ld, int nq, long prows) {       \
-    bwd_pre<D>(o, dout, lse, ld, nq, prows);                                                    \
-  }                                                                                             \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
   void teeny_fa2_bwd_dkdv_bf16_d##D##_c(const bf16* q, const bf16* k, const bf16* v,           \
                                         const bf16* dout, const float* ld, bf16* dk, bf16* dv,  \
@@ -608,17 +606,17 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
   void teeny_fa2_bwd_dq_bf16_d##D##_c(const bf16* q, const bf16* k, const bf16* v,             \
-                                      const bf16* dout, const float* ld, bf16* dq, int nq,      \
-                                      int nk, float scale, int hq, int hkv, int nmb,            \
-                                      int total) {                                              \
-    fa2_bwd_dq<D, true>(q, k, v, dout, ld, dq, nq, nk, scale, hq, hkv, nmb, total);            \
+                                      const bf16* o, const bf16* dout, const float* lse,        \
+                                      float* ld, bf16* dq, int nq, int nk, float scale, int hq, \
+                                      int hkv, int nmb, int total) {                            \
+    fa2_bwd_dq<D, true>(q, k, v, o, dout, lse, ld, dq, nq, nk, scale, hq, hkv, nmb, total);    \
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
   void teeny_fa2_bwd_dq_bf16_d##D##_n(const bf16* q, const bf16* k, const bf16* v,             \
-                                      const bf16* dout, const float* ld, bf16* dq, int nq,      \
-                                      int nk, float scale, int hq, int hkv, int nmb,            \
-                                      int total) {                                              \
-    fa2_bwd_dq<D, false>(q, k, v, dout, ld, dq, nq, nk, scale, hq, hkv, nmb, total);           \
+                                      const bf16* o, const bf16* dout, const float* lse,        \
+                                      float* ld, bf16* dq, int nq, int nk, float scale, int hq, \
+                                      int hkv, int nmb, int total) {                            \
+    fa2_bwd_dq<D, false>(q, k, v, o, dout, lse, ld, dq, nq, nk, scale, hq, hkv, nmb, total);   \
   }
 
 TEENY_FA2_BWD_BF16_INST(64)
