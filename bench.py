@@ -61,8 +61,10 @@ def main() -> int:
                     help="skip the long-context GQA, Llama block and Llama-8B measurements")
     ap.add_argument("--no-power", action="store_true",
                     help="skip the power / clock sampling phase")
-    ap.add_argument("--bandwidth-only", action="store_true",
-                    help="only the HBM-bound kernels at the Llama-block shapes (one JSON line)")
+    ap.add_argument("--only", choices=["bandwidth", "block", "gqa", "llama8b"],
+                    help="run only one of the secondary measurements (one JSON line): the "
+                         "HBM-bound kernels at the Llama-block shapes, one Llama block, the "
+                         "long-context GQA FA2, or the Llama-8B-shape prefill + decode")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed steps, run one head transpose (a pure copy) of "
                          "Q's 256 MiB, the known-size reference for HBM byte counters")
@@ -80,8 +82,12 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     _lib.lib()
-    if args.bandwidth_only:
-        print(json.dumps({"bandwidth_c2": bench_bandwidth(torch, ops, _lib)}), flush=True)
+    if args.only:
+        run = {"bandwidth": ("bandwidth_c2", lambda: bench_bandwidth(torch, ops, _lib)),
+               "block": ("llama_block", lambda: bench_llama_block(torch)),
+               "gqa": ("fa2_gqa_long", lambda: bench_gqa_long(torch, ops)),
+               "llama8b": ("llama_8b_shape", lambda: bench_llama_8b(torch))}[args.only]
+        print(json.dumps({run[0]: run[1]()}), flush=True)
         return 0
     gen = torch.Generator(device=dev).manual_seed(1234)
     shape = (B, H, S, D)

@@ -75,13 +75,12 @@ DEVI void dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voff, int soff) {
 //            banks.  D = 128: x = (r&3)<<2 | (r>>2)&3 (one row per line);
 //            D = 64: two rows per line, x = (line&1)<<2 | (line>>1)&3.
 // Both repeat every 16 rows for D in {64, 128} and every 256 chunks.
-enum Swz { SWZ_ROW, SWZ_DUAL, SWZ_TR8 };
+enum Swz { SWZ_ROW, SWZ_DUAL };
 template <Swz S, int D>
 DEVI int swz(int L) {
   const int line = L >> 4, pos = L & 15;
   int x;
   if (S == SWZ_ROW) x = line & 15;
-  else if (S == SWZ_TR8) x = (line & 3) << 1;
   else if (D == 128) x = ((line & 3) << 2) | ((line >> 2) & 3);
   else x = ((line & 1) << 2) | ((line >> 1) & 3);
   return (line << 4) | (pos ^ x);

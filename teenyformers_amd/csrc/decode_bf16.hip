@@ -22,9 +22,9 @@ constexpr int TK = 32;  // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
-// s_waitcnt immediate: vmcnt(n) (6 bits, split over [3:0] and [15:14]),
-// expcnt and lgkmcnt not waited for
-constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+// s_waitcnt immediate for vmcnt(0) alone (expcnt and lgkmcnt fields at their
+// maximum: not waited for)
+constexpr int kVmcnt0 = (7 << 4) | (15 << 8);
 
 template <int D>
 struct __attribute__((aligned(16))) DecSmem {
@@ -118,7 +118,7 @@ __device__ void decode_mfma(const bf16* __restrict__ q, const bf16* __restrict__
     // tile it has landed; tile it + 1 streams in while it is used.  (Waiting
     // for a partial count here instead made the compiler add a wait for
     // every LDS load in flight before the first LDS read.)
-    __builtin_amdgcn_s_waitcnt(vm_wait(0));
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
     if (it + 1 < n_tiles) load(t0 + TK, buf ^ 1);
     const char* kt = sm.k[buf];
     const char* vt = sm.v[buf];
