@@ -30,6 +30,8 @@
 // are masked.
 #include "cdna4.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int BN = 128;  // keys per workgroup
@@ -551,26 +553,46 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  int kcur = 0, vcur = 0;                     // byte offsets of tile it's buffers
-  int kprev = (QKBUF - 1) * TILE + HALF;      // K half whose dS^T is pending
-  for (int it = 0; it < n_iter; ++it) {
-    if (it + 1 < n_iter) load_tile(it + 1, next_buf(kcur, QKBUF), next_buf(vcur, QVBUF));
+  // Tile it uses K buffer it % 3 and V buffer it % 2.  The loop is unrolled
+  // over the 6 tiles after which both rotations repeat, so every LDS address
+  // is a lane offset plus a constant (the read's immediate offset) instead of
+  // one address add per read.
+  auto tile_step = [&](int it, auto KB, auto VB) {
+    constexpr int kb = decltype(KB)::value, vb = decltype(VB)::value;
+    if (it + 1 < n_iter) load_tile(it + 1, ((kb + 1) % QKBUF) * TILE, ((vb + 1) % QVBUF) * TILE);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       f32x16 s, dp;
-      s_dp(sm.k[0] + kcur + u * HALF, sm.v[0] + vcur + u * HALF, s, dp);
+      s_dp(sm.k[kb] + u * HALF, sm.v[vb] + u * HALF, s, dp);
       mask(it * QBN + 32 * u, s);
-      dq_and_ds(sm.k[0] + kprev, s, dp);
-      kprev = kcur + u * HALF;
+      // the pending dS^T is of the previous half: tile it-1's second half, then this tile's first
+      dq_and_ds(u == 0 ? sm.k[(kb + QKBUF - 1) % QKBUF] + HALF : sm.k[kb], s, dp);
     }
-    kcur = next_buf(kcur, QKBUF);
-    vcur = next_buf(vcur, QVBUF);
     __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile it+1 have landed
     __syncthreads();
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  int it = 0;
+  for (; it + 6 <= n_iter; it += 6) {
+    tile_step(it, I0{}, I0{});
+    tile_step(it + 1, I1{}, I1{});
+    tile_step(it + 2, I2{}, I0{});
+    tile_step(it + 3, I0{}, I1{});
+    tile_step(it + 4, I1{}, I0{});
+    tile_step(it + 5, I2{}, I1{});
   }
-  if (n_iter > 0) {
+  // the last n_iter % 6 tiles (same buffer sequence)
+  if (it < n_iter) tile_step(it, I0{}, I0{});
+  if (it + 1 < n_iter) tile_step(it + 1, I1{}, I1{});
+  if (it + 2 < n_iter) tile_step(it + 2, I2{}, I0{});
+  if (it + 3 < n_iter) tile_step(it + 3, I0{}, I1{});
+  if (it + 4 < n_iter) tile_step(it + 4, I1{}, I0{});
+  if (n_iter > 0) {  // tile n_iter-1's second half: its dS^T product is pending
+    const char* kl = sm.k[0] + ((n_iter - 1) % QKBUF) * TILE + HALF;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) dq_mfma(j, dq_read(sm.k[0] + kprev, j));
+    for (int j = 0; j < NJ; ++j) dq_mfma(j, dq_read(kl, j));
   }
 
   if (qok) {

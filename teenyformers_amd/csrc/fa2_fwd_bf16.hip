@@ -37,6 +37,8 @@
 //     (K/V stay in that XCD's L2), heaviest causal blocks first.
 #include "cdna4.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int BM = 128;  // query rows per workgroup
@@ -133,7 +135,12 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   // K: lane reads row 32*kt + l32, column chunk 2c + g.
   int k_off[DC];
 #pragma unroll
-  for (int c = 0; c < DC; ++c) k_off[c] = swz<SWZ_ROW, D>(l32 * CPR + 2 * c + g) * 16;
+  for (int c = 0; c < DC; ++c) {
+    k_off[c] = swz<SWZ_ROW, D>(l32 * CPR + 2 * c + g) * 16;
+    // opaque to the optimiser: known-zero high bits would turn buffer base +
+    // offset into an OR, which is not folded into the read's immediate offset
+    pin(k_off[c]);
+  }
   // V^T: lane p of 16-lane group G reads row 4g + p/4 (+8, +16hh, +32kt) and
   // 8 bytes at column 32t + 16(G%2) + 4(p%4); rows differing by 8 share the
   // swizzle, so only the column tile t needs its own offset.
@@ -146,6 +153,7 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
       const int row = 8 * e + 4 * g + ((lane & 15) >> 2);
       const int col = 32 * t + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
       v_off[t][e] = swz<SWZ_DUAL, D>(row * CPR + col / 8) * 16 + (col % 8) * 2;
+      pin(v_off[t][e]);
     }
   constexpr int ROW8 = 8 * D * 2;  // bytes of 8 rows (a swizzle-invariant step)
 
@@ -282,9 +290,6 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
     for (int t = 0; t < DT; ++t) acc_o[t] *= alpha;
   };
 
-  // LDS tile buffers rotate through wrapping byte offsets (not it % n, which
-  // loop strength reduction turns into one address register per read)
-  auto next_buf = [](int off, int n) { return off + TILE == n * TILE ? 0 : off + TILE; };
 
   // ---- first tile: scores and P only ----
   if (n_iter > 0) {
@@ -308,20 +313,24 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
 
   // ---- steady state: QK of tile it; then the PV product of tile it-1 on the
   //      matrix cores interleaved with tile it's softmax on the VALU ----
-  // byte offsets of K tile it, V tile it-1 and V tile it+1 in their buffers
-  int kcur = TILE, vprev = 0, vnext = 2 * TILE;
-  for (int it = 1; it < n_iter; ++it) {
+  // Tile it's K sits in buffer it % 2, its V in buffer it % 3.  The loop is
+  // unrolled over the 6 tiles after which both rotations repeat, so every LDS
+  // address is a lane offset plus a constant (the read's immediate offset)
+  // instead of one address add per read.
+  auto tile_step = [&](int it, auto KB, auto VP) {
+    constexpr int kb = decltype(KB)::value;  // K buffer of tile it
+    constexpr int vp = decltype(VP)::value;  // V buffer of tile it - 1
     const int kbase = it * BN;
-    if (it + 1 < n_iter) load_tile(it + 1, next_buf(kcur, KBUF), vnext);
+    if (it + 1 < n_iter) load_tile(it + 1, ((kb + 1) % KBUF) * TILE, ((vp + 2) % VBUF) * TILE);
     f32x16 s0, s1;
-    qk(sm.k[0] + kcur, s0, s1);
+    qk(sm.k[kb], s0, s1);
     mask(kbase, s0, s1);
     // a maximum raised by tile it-1 scales O before tile it-1's product
     if (grow) rescale_o();
 
     // issue order, fenced: V reads VPF products ahead; each product followed
     // by its share of the VALU work (row max first, then the exponentials)
-    const char* vt = sm.v[0] + vprev;
+    const char* vt = sm.v[vp];
     u32x4 va[NJ];
 #pragma unroll
     for (int j = 0; j < VPF; ++j) va[j] = pv_read(vt, j);
@@ -343,16 +352,32 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
     }
     pin(l_run);
     pin(l_run2);
-    kcur = next_buf(kcur, KBUF);
-    vprev = next_buf(vprev, VBUF);
-    vnext = next_buf(vnext, VBUF);
-
     __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile it+1 have landed
     __syncthreads();
+  };
+  {
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    int it = 1;
+    for (; it + 6 <= n_iter; it += 6) {
+      tile_step(it, I1{}, I0{});
+      tile_step(it + 1, I0{}, I1{});
+      tile_step(it + 2, I1{}, I2{});
+      tile_step(it + 3, I0{}, I0{});
+      tile_step(it + 4, I1{}, I1{});
+      tile_step(it + 5, I0{}, I2{});
+    }
+    // the last (n_iter - 1) % 6 tiles (same buffer sequence)
+    if (it < n_iter) tile_step(it, I1{}, I0{});
+    if (it + 1 < n_iter) tile_step(it + 1, I0{}, I1{});
+    if (it + 2 < n_iter) tile_step(it + 2, I1{}, I2{});
+    if (it + 3 < n_iter) tile_step(it + 3, I0{}, I0{});
+    if (it + 4 < n_iter) tile_step(it + 4, I1{}, I1{});
   }
   if (n_iter > 0) {
     if (grow) rescale_o();
-    const char* vt = sm.v[0] + vprev;
+    const char* vt = sm.v[0] + ((n_iter - 1) % VBUF) * TILE;  // tile n_iter-1's V
 #pragma unroll
     for (int j = 0; j < NJ; ++j) pv_mfma(j, pv_read(vt, j));
   }
