@@ -122,6 +122,23 @@ DEVI float wave_max(float v) {
   return v;
 }
 
+// Order of the (head, block) work items behind the remapped ids: heads two
+// at a time, the blocks of a pair interleaved heaviest first.  Causal blocks
+// differ in cost by up to n_blocks x; taken head by head (heaviest first),
+// the heaviest blocks of an XCD's last head started last and finished ~5 %
+// after the rest at 32 blocks per head, while pairs keep the workgroups in
+// flight on ~2 heads' K/V as before.  Pairs only when every XCD's contiguous
+// share of ids holds whole pairs (n_heads a multiple of 16): a pair split
+// between two XCDs would hand one of them all the heavy blocks.  rank 0 is a
+// head's heaviest block.  Bijective on [0, n_heads * n_blocks).
+DEVI void pair_order(int id, int n_blocks, int n_heads, int& head, int& rank) {
+  const int gsz = n_heads % (2 * TEENY_NUM_XCD) == 0 ? 2 : 1;
+  const int grp = id / (gsz * n_blocks);
+  const int r = id - grp * gsz * n_blocks;
+  head = gsz * grp + r % gsz;
+  rank = r / gsz;
+}
+
 // Remap a linear workgroup id so that consecutive ids in the returned space
 // land on the same XCD (the hardware deals ids round-robin across XCDs).
 // Bijective for any total.

@@ -73,8 +73,9 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   const int l32 = lane & 31, g = lane >> 5;
 
   const int id = xcd_remap(blockIdx.x, total_blocks);
-  const int bh = id / num_m_blocks;
-  const int mb = num_m_blocks - 1 - (id - bh * num_m_blocks);
+  int bh, rank;
+  pair_order(id, num_m_blocks, total_blocks / num_m_blocks, bh, rank);
+  const int mb = num_m_blocks - 1 - rank;  // the last query block is the heaviest
   const int b = bh / hq, h = bh - b * hq;
   const long kvh = (long)b * hkv + h / (hq / hkv);
   const int m0 = mb * BM;
