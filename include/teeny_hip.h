@@ -212,9 +212,9 @@ int teeny_token_embed_fwd(const void* ids, const void* weight, void* out, int se
  *   with their arithmetic (transpose_heads.rs:65-67, rope.rs:86-96).
  * teeny_decode_attention: one query row per (b, q head), q [B, Hq, D],
  *   against cache rows 0 .. n_keys-1 (all visible: the newest query is the
- *   last position), o [B, Hq, D].  Split-K over 256-key chunks; workspace
- *   teeny_decode_attention_workspace_bytes(...).  The reference recomputes
- *   the prefix instead (examples/llama_generate.rs:373-381).
+ *   last position), o [B, Hq, D].  Split over the keys; workspace of
+ *   teeny_decode_attention_workspace_bytes(...) bytes.  The reference
+ *   recomputes the prefix instead (examples/llama_generate.rs:373-381).
  *   head_dim: a power of two from 8 to 128; Hq / Hkv <= 16.
  * ------------------------------------------------------------------------ */
 int teeny_qkv_rope_split(const void* qkv, void* q_out, void* k_cache, void* v_cache, int batch,
@@ -271,7 +271,7 @@ int teeny_linear_swiglu_bf16(const void* x, const void* w, void* y, int M, int F
 
 /* The same product split over K for more parallelism at small N: writes
  * teeny_linear_partials_count(K, k_split) fp32 slabs parts[n][M][N], slab i
- * summing k in [i k_split, (i+1) k_split).  k_split is a multiple of 512 or
+ * summing k in [i k_split, (i+1) k_split).  k_split is a multiple of 128 or
  * >= K.  The slabs are consumed, summed in slab order and rounded to the
  * activation dtype (as the unsplit product would be stored), by
  * teeny_fused_add_rmsnorm_partials_fwd (x = the sum; otherwise as

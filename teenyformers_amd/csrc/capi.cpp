@@ -839,7 +839,7 @@ int teeny_linear_partials_bf16(const void* x, const void* w, float* parts, int M
   if (rc) return rc;
   if (k_split <= 0) return TEENY_ERR_INVALID_VALUE;
   if (k_split >= K) k_split = K;
-  else if (k_split % 512 != 0) return TEENY_ERR_INVALID_VALUE;  // whole staged x chunks
+  else if (k_split % 128 != 0) return TEENY_ERR_INVALID_VALUE;  // whole 128-wide K steps
   const int n = teeny_linear_partials_count(K, k_split);
   if (n > 65535) return TEENY_ERR_INVALID_SHAPE;
   void* args[] = {&x, &w, &parts, &M, &N, &K, &k_split};

@@ -75,39 +75,50 @@ template <> struct Vec16<bf16> {
 
 // VEC consecutive values of a sum of n fp32 partial slabs (slab s at
 // part + s * stride), added in slab order and rounded to T: what a product
-// split over K gives once its parts are summed and stored in T.
+// split over K gives once its parts are summed and stored in T.  CH chunks
+// at part + off[c] are summed at once.  The loads of a group of U slabs are
+// all issued before the first add (unconditionally: slabs past n re-read slab
+// n - 1 and are not added), so a call waits for memory once per group.
+template <typename T, int VEC, int CH>
+DEVI void ld_parts(const float* __restrict__ part, long stride, int n, float (*out)[VEC],
+                   const int* off) {
+  static_assert(VEC % 4 == 0, "16-byte loads");
+  constexpr int U = CH >= 4 ? 4 : 8;  // slabs in flight together
+  float acc[CH][VEC];
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) acc[c][j] = 0.0f;
+  for (int s = 0; s < n; s += U) {
+    f32x4 v[U][CH][VEC / 4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float* src = part + min(s + u, n - 1) * stride;
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int j = 0; j < VEC / 4; ++j)
+          v[u][c][j] = *reinterpret_cast<const f32x4*>(src + off[c] + 4 * j);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (s + u < n)
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+          for (int j = 0; j < VEC / 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[c][4 * j + i] += v[u][c][j][i];
+  }
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) out[c][j] = (float)(T)acc[c][j];
+}
 template <typename T, int VEC>
 DEVI void ld_parts(const float* __restrict__ part, long stride, int n, float* out) {
-  static_assert(VEC % 4 == 0, "16-byte loads");
-  constexpr int U = 8;  // slabs whose loads are in flight together
-  float acc[VEC];
-#pragma unroll
-  for (int j = 0; j < VEC; ++j) acc[j] = 0.0f;
-  int s = 0;
-  for (; s + U <= n; s += U) {
-    f32x4 v[U][VEC / 4];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int j = 0; j < VEC / 4; ++j)
-        v[u][j] = *reinterpret_cast<const f32x4*>(part + (s + u) * stride + 4 * j);
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int j = 0; j < VEC / 4; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[4 * j + i] += v[u][j][i];
-  }
-  for (; s < n; ++s) {
-#pragma unroll
-    for (int j = 0; j < VEC / 4; ++j) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(part + s * stride + 4 * j);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[4 * j + i] += v[i];
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < VEC; ++j) out[j] = (float)(T)acc[j];
+  const int off[1] = {0};
+  ld_parts<T, VEC, 1>(part, stride, n, reinterpret_cast<float(*)[VEC]>(out), off);
 }
 
 // Wavefront (64-lane) reductions through DPP/permute, all lanes get the result.

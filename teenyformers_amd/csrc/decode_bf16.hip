@@ -122,10 +122,15 @@ __device__ void decode_mfma(const bf16* __restrict__ q, const bf16* __restrict__
     if (it + 1 < n_tiles) load(t0 + TK, buf ^ 1);
     const char* kt = sm.k[buf];
     const char* vt = sm.v[buf];
+    // all K reads first (one LDS latency per tile, not one per product)
+    u32x4 kr[DC];
+#pragma unroll
+    for (int c = 0; c < DC; ++c) kr[c] = *reinterpret_cast<const u32x4*>(kt + k_off[c]);
     f32x16 s = f32x16{};
 #pragma unroll
-    for (int c = 0; c < DC; ++c)
-      s = mfma32(as_bf16x8(*reinterpret_cast<const u32x4*>(kt + k_off[c])), qreg[c], s);
+    for (int c = 0; c < DC; ++c) s = mfma32(as_bf16x8(kr[c]), qreg[c], s);
+    sched_group(kDsRead, DC);
+    sched_group(kMfma, DC);
 #pragma unroll
     for (int r = 0; r < 16; ++r)
       if (t0 + 8 * (r >> 2) + 4 * g + (r & 3) >= k1) s[r] = -INFINITY;
@@ -175,7 +180,8 @@ __device__ void decode_mfma(const bf16* __restrict__ q, const bf16* __restrict__
 }  // namespace
 
 #define TEENY_DECODE_BF16_INST(D)                                                                \
-  extern "C" __global__ __launch_bounds__(64) void teeny_decode_mfma_bf16_d##D(                \
+  extern "C" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))          \
+  void teeny_decode_mfma_bf16_d##D(                                                             \
       const bf16* q, const bf16* kc, const bf16* vc, float* pm, float* pl, float* po, int hq,    \
       int hkv, const int* n_past, int n_keys, int cache_len, int keys_per_split, float scale) {  \
     decode_mfma<D>(q, kc, vc, pm, pl, po, hq, hkv, n_past, n_keys, cache_len, keys_per_split,   \

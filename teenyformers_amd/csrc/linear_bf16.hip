@@ -43,7 +43,7 @@ DEVI f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
 enum SkMode { SK_BF16, SK_SWIGLU, SK_PART };
 
 // K % 128 == 0; the K range of a workgroup is [blockIdx.y * KC, +KC) with
-// KC % XC == 0 (or KC == K); its last chunk may hold fewer than 4 steps.
+// KC % 128 == 0 (or KC == K); its last chunk may hold fewer than 4 steps.
 template <SkMode MODE>
 __device__ void linear_sk(const bf16* __restrict__ x, const bf16* __restrict__ w,
                           void* __restrict__ out, int M, int N, int K, int KC) {

@@ -248,20 +248,45 @@ __device__ void decode_partial(const T* __restrict__ q, const T* __restrict__ kc
   }
 }
 
-// grid B*Hq, block head_dim threads: merge the chunk partials.
+// grid B*Hq, block head_dim threads: merge the chunk partials.  The partials
+// of kGroup chunks are loaded together (one memory wait per group) and folded
+// into a running maximum: acc and l are scaled by e^(m_old - m_new) when a
+// group raises it.
 template <typename T>
 __device__ void decode_combine(const float* __restrict__ pm, const float* __restrict__ pl,
                                const float* __restrict__ po, T* __restrict__ o, int n_chunks,
                                int head_dim) {
+  constexpr int kGroup = 16;
   const long row = blockIdx.x;
   const int d = threadIdx.x;
-  float m = -INFINITY;
-  for (int c = 0; c < n_chunks; ++c) m = fmaxf(m, pm[row * n_chunks + c]);
-  float l = 0.0f, acc = 0.0f;
-  for (int c = 0; c < n_chunks; ++c) {
-    float w = expf(pm[row * n_chunks + c] - m);
-    l += pl[row * n_chunks + c] * w;
-    acc += po[(row * n_chunks + c) * head_dim + d] * w;
+  const float* rm = pm + row * n_chunks;
+  const float* rl = pl + row * n_chunks;
+  const float* ro = po + row * n_chunks * head_dim + d;
+  float m = -INFINITY, l = 0.0f, acc = 0.0f;
+  for (int c0 = 0; c0 < n_chunks; c0 += kGroup) {
+    float mv[kGroup], lv[kGroup], ov[kGroup];
+#pragma unroll
+    for (int c = 0; c < kGroup; ++c) {  // chunks past the end re-read the last one
+      const int cc = min(c0 + c, n_chunks - 1);
+      mv[c] = rm[cc];
+      lv[c] = rl[cc];
+      ov[c] = ro[(long)cc * head_dim];
+    }
+    float gm = m;
+#pragma unroll
+    for (int c = 0; c < kGroup; ++c) gm = fmaxf(gm, mv[c]);
+    if (gm == -INFINITY) continue;  // no keys yet
+    const float r = expf(m - gm);   // 0 while m is -inf
+    l *= r;
+    acc *= r;
+#pragma unroll
+    for (int c = 0; c < kGroup; ++c)
+      if (c0 + c < n_chunks) {
+        const float w = expf(mv[c] - gm);
+        l += lv[c] * w;
+        acc += ov[c] * w;
+      }
+    m = gm;
   }
   o[row * head_dim + d] = (T)(acc / l);
 }

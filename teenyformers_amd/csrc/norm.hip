@@ -211,21 +211,36 @@ __device__ void rmsnorm_fwd_row_wg(const T* __restrict__ x, const T* __restrict_
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
   const long base = (long)row * N;
-  float hv[CH][VEC];
-  float sq = 0.0f;
+  // the weight and residual loads go out first, then x (or its slabs): the
+  // row waits for memory once
+  float wv[CH][VEC], rv[CH][VEC];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     int idx = (c * 256 + tid) * VEC;
     if (idx < N) {
-      if constexpr (PARTS)
-        ld_parts<T, VEC>(xparts + base + idx, (long)gridDim.x * N, n_parts, hv[c]);
-      else
-        ldv<T, VEC>(x + base + idx, hv[c]);
-      if (res) {
-        float rv[VEC];
-        ldv<T, VEC>(res + base + idx, rv);
+      ldv<T, VEC>(w + idx, wv[c]);
+      if (res) ldv<T, VEC>(res + base + idx, rv[c]);
+    }
+  }
+  float hv[CH][VEC];
+  float sq = 0.0f;
+  if constexpr (PARTS) {  // every chunk's slab loads in flight together
+    int off[CH];            // chunks past the row re-read its first element
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) hv[c][j] += rv[j];
+    for (int c = 0; c < CH; ++c) {
+      const int idx = (c * 256 + tid) * VEC;
+      off[c] = idx < N ? idx : 0;
+    }
+    ld_parts<T, VEC, CH>(xparts + base, (long)gridDim.x * N, n_parts, hv, off);
+  }
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    int idx = (c * 256 + tid) * VEC;
+    if (idx < N) {
+      if constexpr (!PARTS) ldv<T, VEC>(x + base + idx, hv[c]);
+      if (res) {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) hv[c][j] += rv[c][j];
       }
 #pragma unroll
       for (int j = 0; j < VEC; ++j) sq += hv[c][j] * hv[c][j];
@@ -235,12 +250,6 @@ __device__ void rmsnorm_fwd_row_wg(const T* __restrict__ x, const T* __restrict_
         for (int j = 0; j < VEC; ++j) hv[c][j] = (float)(T)hv[c][j];
       }
     }
-  }
-  float wv[CH][VEC];
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    int idx = (c * 256 + tid) * VEC;
-    if (idx < N) ldv<T, VEC>(w + idx, wv[c]);
   }
   sq = wave_sum(sq);
   if ((tid & 63) == 0) part[tid >> 6] = sq;

@@ -476,16 +476,20 @@ class Partials:
 
 
 def _k_split(K: int, N: int) -> int:
-    """K per slab, in whole 512-wide chunks: enough slabs that the 128-feature
-    workgroups fill the GPU (about 256), at most 8 (each slab costs the
-    consumer a read)."""
-    splits = min(8, max(-(-256 // (N // 128)), -(-K // (7 * 512))))
-    return max(512, -(-K // (splits * 512)) * 512)
+    """K per slab, in whole 128-wide steps.  The 128-feature workgroups times
+    the slabs are spread over 256 CUs; the slab count (at most 16) minimises
+    the busiest CU's work, ceil(workgroups / 256) * (steps per slab + 2), the
+    2 standing for a workgroup's fixed cost, and ties go to fewer slabs (each
+    slab costs the consumer a read)."""
+    rows, steps = N // 128, K // 128
+    best = min(range(1, 17), key=lambda n: (-(-rows * n // 256) * (-(-steps // n) + 2), n))
+    return -(-steps // best) * 128
 
 
-def linear_split(x: torch.Tensor, w: torch.Tensor):
+def linear_split(x: torch.Tensor, w: torch.Tensor, k_split: int | None = None):
     """x w^T as Partials where the decode kernels take the shape (up to 16
-    bf16 rows), else the GEMM's tensor."""
+    bf16 rows), else the GEMM's tensor.  k_split (a multiple of 128) sets K
+    per slab; by default it is chosen to spread the work over the CUs."""
     x2 = x.reshape(-1, x.shape[-1])
     N, K = w.shape
     if K != x2.shape[1]:
@@ -493,7 +497,7 @@ def linear_split(x: torch.Tensor, w: torch.Tensor):
     if not _skinny(x2, w, N):
         return torch.nn.functional.linear(x, w)
     x2 = x2.contiguous()
-    ks = _k_split(K, N)
+    ks = _k_split(K, N) if k_split is None else k_split
     n = _lib.lib().teeny_linear_partials_count(K, ks)
     slabs = torch.empty((n, x2.shape[0], N), dtype=torch.float32, device=x.device)
     call("teeny_linear_partials_bf16", _p(x2), _p(w), _p(slabs), x2.shape[0], N, K, ks,

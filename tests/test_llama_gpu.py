@@ -258,25 +258,27 @@ def _seq_sum_bf16(slabs):
     return O.bf16_round(acc)
 
 
-def test_partials_consumers_bit_exact(cuda):
+@pytest.mark.parametrize("d,k_split", [
+    (2048, None), (2048, 384), (2048, 128),  # 16, 6 (a last group of 6) and 16 slabs
+    (4096, 640), (8192, 1152)])              # 7 and 8 slabs of 2 and 4 chunks per thread
+def test_partials_consumers_bit_exact(cuda, d, k_split):
     """The residual-add norm and the QKV split read K-split slabs exactly as
     they read the stored bf16 product."""
-    rng = np.random.default_rng(11)
+    rng = np.random.default_rng(11 + d + (k_split or 0))
     B, Hq, Hkv, D, L = 4, 8, 2, 64, 64
-    d = 2048
     n = (Hq + 2 * Hkv) * D
     x = _bf16_dev(rng.standard_normal((B, d)).astype(np.float32))
     wq = _bf16_dev((0.02 * rng.standard_normal((n, d))).astype(np.float32))
     wo = _bf16_dev((0.02 * rng.standard_normal((d, d))).astype(np.float32))
     res = _bf16_dev(rng.standard_normal((B, d)).astype(np.float32))
     gamma = _bf16_dev((1 + 0.1 * rng.standard_normal(d)).astype(np.float32))
-    po = ops.linear_split(x, wo)
+    po = ops.linear_split(x, wo, k_split)
     assert po.n > 1
     a = _bf16_dev(_seq_sum_bf16(po.slabs.cpu().numpy()))
     y1, h1, r1 = ops.fused_add_rmsnorm(po, res, gamma, 1e-5)
     y2, h2, r2 = ops.fused_add_rmsnorm(a, res, gamma, 1e-5)
     assert torch.equal(y1, y2) and torch.equal(h1, h2) and torch.equal(r1, r2)
-    pq = ops.linear_split(x.view(B, 1, d), wq)
+    pq = ops.linear_split(x.view(B, 1, d), wq, k_split)
     qkv = _bf16_dev(_seq_sum_bf16(pq.slabs.cpu().numpy())).view(B, 1, n)
     pos = torch.tensor([17], dtype=torch.int32, device="cuda")
     outs = []
