@@ -188,7 +188,6 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
       nqb = qb_first;
       ++nhead;
     }
-    if (it + 1 < n_iter) load_tile(nhead, nqb, buf ^ 1);
     const char* qt = sm.q[buf];
     const char* dt = sm.d[buf];
     const float* lt = sm.ld[buf];
@@ -212,6 +211,7 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
         sched_group(kMfma, 1);
       }
     }
+    if (it + 1 < n_iter) load_tile(nhead, nqb, buf ^ 1);  // after the S products
     // ---- masking (boundary blocks only): scores -> -inf, so P = dS = 0 ----
     if ((kw0 + 32 > nk) || (CAUSAL && kw0 + 31 > qb0)) {
 #pragma unroll
@@ -560,11 +560,12 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   // one address add per read.
   auto tile_step = [&](int it, auto KB, auto VB) {
     constexpr int kb = decltype(KB)::value, vb = decltype(VB)::value;
-    if (it + 1 < n_iter) load_tile(it + 1, ((kb + 1) % QKBUF) * TILE, ((vb + 1) % QVBUF) * TILE);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       f32x16 s, dp;
       s_dp(sm.k[kb] + u * HALF, sm.v[vb] + u * HALF, s, dp);
+      if (u == 0 && it + 1 < n_iter)  // after the first products (as in the forward)
+        load_tile(it + 1, ((kb + 1) % QKBUF) * TILE, ((vb + 1) % QVBUF) * TILE);
       mask(it * QBN + 32 * u, s);
       // the pending dS^T is of the previous half: tile it-1's second half, then this tile's first
       dq_and_ds(u == 0 ? sm.k[(kb + QKBUF - 1) % QKBUF] + HALF : sm.k[kb], s, dp);

@@ -322,9 +322,11 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
     constexpr int kb = decltype(KB)::value;  // K buffer of tile it
     constexpr int vp = decltype(VP)::value;  // V buffer of tile it - 1
     const int kbase = it * BN;
-    if (it + 1 < n_iter) load_tile(it + 1, ((kb + 1) % KBUF) * TILE, ((vp + 2) % VBUF) * TILE);
     f32x16 s0, s1;
     qk(sm.k[kb], s0, s1);
+    // tile it+1's loads go out after the score products, not before them:
+    // the burst of DMA issues then does not hold up the first MFMAs
+    if (it + 1 < n_iter) load_tile(it + 1, ((kb + 1) % KBUF) * TILE, ((vp + 2) % VBUF) * TILE);
     mask(kbase, s0, s1);
     // a maximum raised by tile it-1 scales O before tile it-1's product
     if (grow) rescale_o();
