@@ -97,7 +97,7 @@ def main() -> int:
     o = torch.empty_like(q)
     lse = torch.empty((B, H, S), dtype=torch.float32, device=dev)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    ws = torch.empty(ops.flash_attn2_bwd_workspace_bytes(q), dtype=torch.uint8, device=dev)
+    ws = torch.empty(ops.flash_attn2_bwd_workspace_bytes(q, k), dtype=torch.uint8, device=dev)
 
     def step():
         ops.flash_attn2_fwd(q, k, v, scale, True, out=o, lse=lse)

@@ -118,6 +118,15 @@ int teeny_flash_attn2_bwd(const void* q, const void* k, const void* v, const voi
  * (its executor sizes caches from RuntimeOp::param_shapes, flash_attn2.rs:449-457). */
 size_t teeny_flash_attn2_bwd_workspace_bytes(int n_ctx_q, int batch, int n_heads_q, int head_dim,
                                              int dtype);
+/* The workspace that also lets a bf16 GQA backward with few key blocks
+ * (fewer 128-key blocks x batch x kv heads than two per CU) split each
+ * group's q heads over 2 or 4 dK/dV workgroups, whose fp32 partial sums a
+ * merge kernel adds in a fixed order; otherwise equal to the above.  With a
+ * smaller workspace the backward runs unsplit.  No counterpart in the
+ * reference. */
+size_t teeny_flash_attn2_bwd_workspace_bytes_gqa(int n_ctx_q, int n_ctx_k, int batch,
+                                                 int n_heads_q, int n_heads_kv, int head_dim,
+                                                 int dtype);
 
 /* --------------------------------------------------------------------------
  * RoPE on x [BH, n_ctx, head_dim], interleaved pairs, position = row index.

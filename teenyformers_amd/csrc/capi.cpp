@@ -245,6 +245,37 @@ size_t fa2_bwd_ws(int n_ctx_q, int batch, int hq, int head_dim, int dtype) {
   return align256((size_t)batch * hq * n_ctx_q * sizeof(float));
 }
 
+// CUs of the current device (256 on MI355X when it cannot be asked).
+int device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    return 256;
+  return n;
+}
+
+// bf16 dK/dV: into how many workgroups each GQA group's q heads are split.
+// The kernel runs two workgroups per CU and its causal key blocks range
+// from one to n_ctx_q / 128 units of work; with no more workgroups than
+// slots, the heaviest block alone sets the time, so the heads are split
+// (up to 4 ways) while the workgroups still fit twice over.
+int dkdv_hsplit(int n_ctx_k, int batch, int hq, int hkv, int dtype) {
+  if (dtype != TEENY_BF16) return 1;
+  const long slots = 2L * device_cus();
+  long wgs = (long)((n_ctx_k + 127) / 128) * batch * hkv;
+  int split = 1;
+  while (split < 4 && (hq / hkv) % (2 * split) == 0 && wgs <= slots) {
+    split *= 2;
+    wgs *= 2;
+  }
+  return split;
+}
+
+size_t dkdv_split_bytes(int n_ctx_k, int batch, int hkv, int head_dim, int split) {
+  if (split <= 1) return 0;
+  return align256(2 * (size_t)split * batch * hkv * n_ctx_k * head_dim * sizeof(float));
+}
+
 int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void* o,
             const void* dout, const float* l, void* dq, void* dk, void* dv, int n_ctx_q,
             int n_ctx_k, float scale, int batch, int hq, int hkv, int head_dim, int dtype,
@@ -272,15 +303,27 @@ int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void
                   &n_ctx_q, &n_ctx_k, &scale, &hq, &hkv,  &nmb, &tot};
     rc = launch(name, dim3(tot), dim3(256), 0, stream, a2);
     if (rc) return rc;
-    // dK, dV: one workgroup per 128 keys of a (b, kv head)
+    // dK, dV: one workgroup per 128 keys of a (b, kv head) and share of the
+    // group's q heads (the split needs the larger workspace; without it the
+    // heads are not split)
+    int hsplit = dkdv_hsplit(n_ctx_k, batch, hq, hkv, dtype);
+    const size_t base = fa2_bwd_ws(n_ctx_q, batch, hq, head_dim, dtype);
+    if (workspace_bytes < base + dkdv_split_bytes(n_ctx_k, batch, hkv, head_dim, hsplit))
+      hsplit = 1;
+    float* part = hsplit > 1 ? (float*)((char*)workspace + base) : nullptr;
     int nnb = (n_ctx_k + 127) / 128;
-    total = (long)nnb * batch * hkv;
+    total = (long)nnb * batch * hkv * hsplit;
     if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
     tot = (int)total;
     snprintf(name, sizeof name, "teeny_fa2_bwd_dkdv_bf16_d%d_%s", head_dim, cz);
-    void* a1[] = {&q,       &k,       &v,     &dout, &ld,  &dk,  &dv,
-                  &n_ctx_q, &n_ctx_k, &scale, &hq,   &hkv, &nnb, &tot};
-    return launch(name, dim3(tot), dim3(256), 0, stream, a1);
+    void* a1[] = {&q,       &k,       &v,     &dout, &ld,  &dk,  &dv,  &n_ctx_q,
+                  &n_ctx_k, &scale,   &hq,    &hkv,  &nnb, &tot, &hsplit, &part};
+    rc = launch(name, dim3(tot), dim3(256), 0, stream, a1);
+    if (rc || hsplit == 1) return rc;
+    long n = (long)batch * hkv * n_ctx_k * head_dim;  // a multiple of 8
+    void* a3[] = {&part, &dk, &dv, &n, &hsplit, &scale};
+    return launch("teeny_fa2_dkdv_merge_bf16", dim3((unsigned)((n / 8 + 255) / 256)), dim3(256),
+                  0, stream, a3);
   }
   snprintf(name, sizeof name, "teeny_fa2_bwd_pre_f32_d%d", head_dim);
   void* a0[] = {&o, &dout, &delta, (void*)&rows};
@@ -432,6 +475,17 @@ size_t teeny_flash_attn2_bwd_workspace_bytes(int n_ctx_q, int batch, int n_heads
                                              int dtype) {
   if (n_ctx_q <= 0 || batch <= 0 || n_heads_q <= 0 || head_dim <= 0) return 0;
   return fa2_bwd_ws(n_ctx_q, batch, n_heads_q, head_dim, dtype);
+}
+
+size_t teeny_flash_attn2_bwd_workspace_bytes_gqa(int n_ctx_q, int n_ctx_k, int batch,
+                                                 int n_heads_q, int n_heads_kv, int head_dim,
+                                                 int dtype) {
+  if (n_ctx_q <= 0 || n_ctx_k <= 0 || batch <= 0 || n_heads_q <= 0 || n_heads_kv <= 0 ||
+      head_dim <= 0 || n_heads_q % n_heads_kv != 0)
+    return 0;
+  const int split = dkdv_hsplit(n_ctx_k, batch, n_heads_q, n_heads_kv, dtype);
+  return fa2_bwd_ws(n_ctx_q, batch, n_heads_q, head_dim, dtype) +
+         dkdv_split_bytes(n_ctx_k, batch, n_heads_kv, head_dim, split);
 }
 
 static int rope_impl(const void* x, void* y, int n_ctx, float ln_base, int bh, int head_dim,

@@ -54,12 +54,17 @@ struct __attribute__((aligned(16))) DkdvSmem {
   float ld[2][2 * BM];    // LSE * log2(e) and Delta of the tile's rows
 };
 
+// hsplit > 1: the q heads of a GQA group are split over hsplit workgroups
+// (more workgroups when few key blocks would leave CUs idle behind the
+// heaviest causal block); each writes its fp32 dK^T, dV^T sums to
+// part[2][hsplit][B * Hkv][nk][D] (dK unscaled), merged by fa2_dkdv_merge.
 template <int D, bool CAUSAL>
 __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict__ k,
                              const bf16* __restrict__ v, const bf16* __restrict__ dout,
                              const float* __restrict__ ld, bf16* __restrict__ dk,
                              bf16* __restrict__ dv, int nq, int nk, float scale, int hq, int hkv,
-                             int num_n_blocks, int total_blocks) {
+                             int num_n_blocks, int total_blocks, int hsplit,
+                             float* __restrict__ part) {
   constexpr int DC = D / 16;            // d-chunks of 16 (QK^T, dO V^T)
   constexpr int DT = D / 32;            // d-tiles of 32 (dK^T, dV^T)
   constexpr int CPR = D / 8;            // 16-byte chunks per row
@@ -73,10 +78,12 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
   const int l32 = lane & 31, g = lane >> 5;
 
   const int id = xcd_remap(blockIdx.x, total_blocks);
-  int kvh, nb;  // kvh = b * hkv + hk; key block 0 sees the most query rows
-  pair_order(id, num_n_blocks, total_blocks / num_n_blocks, kvh, nb);
+  int hh, nb;  // hh = (b * hkv + hk) * hsplit + hs; key block 0 sees the most query rows
+  pair_order(id, num_n_blocks, total_blocks / num_n_blocks, hh, nb);
+  const int kvh = hh / hsplit, hs = hh - kvh * hsplit;
   const int b = kvh / hkv, hk = kvh - b * hkv;
-  const int group = hq / hkv;
+  const int group = hq / hkv / hsplit;  // q heads walked by this workgroup
+  const int head0 = hk * (hq / hkv) + hs * group;
   const int n0 = nb * BN;
   const int kw0 = n0 + 32 * wave;  // this wave's first key
   const int mykey = kw0 + l32;
@@ -115,7 +122,7 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
   // LSE / Delta (2*BM floats, one dword per lane).
   const uint32_t src = swz<SWZ_DUAL, D>(tid) * 16;
   auto load_tile = [&](int head, int qb, int buf) {
-    const long bh = (long)b * hq + (long)hk * group + head;
+    const long bh = (long)b * hq + head0 + head;
     const int row0 = qb * BM;
     const int bytes = (nq - row0) * D * 2;  // > 0: row0 < nq
     const auto qr = make_rsrc(q + (bh * nq + row0) * D, bytes);
@@ -294,6 +301,24 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
   }
 
   // ---- dK = scale * dK^T, dV = dV^T, lane = key, 16 d values per tile -------
+  if (hsplit > 1) {  // fp32 sums of this workgroup's heads
+    if (mykey < nk) {
+      const long n_kvh = total_blocks / num_n_blocks / hsplit;
+      float* pk = part + (((long)hs * n_kvh + kvh) * nk + mykey) * D;
+      float* pv = pk + (long)hsplit * n_kvh * nk * D;
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = 32 * t + 8 * j + 4 * g;
+          *reinterpret_cast<f32x4*>(pk + d) =
+              f32x4{dk_acc[t][4 * j], dk_acc[t][4 * j + 1], dk_acc[t][4 * j + 2], dk_acc[t][4 * j + 3]};
+          *reinterpret_cast<f32x4*>(pv + d) =
+              f32x4{dv_acc[t][4 * j], dv_acc[t][4 * j + 1], dv_acc[t][4 * j + 2], dv_acc[t][4 * j + 3]};
+        }
+    }
+    return;
+  }
   if (mykey < nk) {
     bf16* dkr = dk + ((long)kvh * nk + mykey) * D;
     bf16* dvr = dv + ((long)kvh * nk + mykey) * D;
@@ -309,6 +334,32 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
             u32x2{pack_bf16x2(dv_acc[t][4 * j], dv_acc[t][4 * j + 1]),
                   pack_bf16x2(dv_acc[t][4 * j + 2], dv_acc[t][4 * j + 3])};
       }
+  }
+}
+
+// dK = scale * sum of the hsplit partial dK^T, dV = sum of the dV^T, in
+// split order; n = B * Hkv * nk * D (a multiple of 8), 8 values per thread.
+__device__ void fa2_dkdv_merge(const float* __restrict__ part, bf16* __restrict__ dk,
+                               bf16* __restrict__ dv, long n, int hsplit, float scale) {
+  const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i >= n) return;
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const float* src = part + (long)w * hsplit * n + i;
+    float acc[8];
+    Vec16<float>::load(src, acc);
+    Vec16<float>::load(src + 4, acc + 4);
+    for (int s = 1; s < hsplit; ++s) {
+      float a[8];
+      Vec16<float>::load(src + (long)s * n, a);
+      Vec16<float>::load(src + (long)s * n + 4, a + 4);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += a[j];
+    }
+    if (w == 0)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] *= scale;
+    Vec16<bf16>::store((w == 0 ? dk : dv) + i, acc);
   }
 }
 
@@ -618,15 +669,17 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   void teeny_fa2_bwd_dkdv_bf16_d##D##_c(const bf16* q, const bf16* k, const bf16* v,           \
                                         const bf16* dout, const float* ld, bf16* dk, bf16* dv,  \
                                         int nq, int nk, float scale, int hq, int hkv, int nnb,  \
-                                        int total) {                                            \
-    fa2_bwd_dkdv<D, true>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb, total);      \
+                                        int total, int hsplit, float* part) {                   \
+    fa2_bwd_dkdv<D, true>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb, total,       \
+                          hsplit, part);                                                        \
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
   void teeny_fa2_bwd_dkdv_bf16_d##D##_n(const bf16* q, const bf16* k, const bf16* v,           \
                                         const bf16* dout, const float* ld, bf16* dk, bf16* dv,  \
                                         int nq, int nk, float scale, int hq, int hkv, int nnb,  \
-                                        int total) {                                            \
-    fa2_bwd_dkdv<D, false>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb, total);     \
+                                        int total, int hsplit, float* part) {                   \
+    fa2_bwd_dkdv<D, false>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb, total,      \
+                           hsplit, part);                                                       \
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
   void teeny_fa2_bwd_dq_bf16_d##D##_c(const bf16* q, const bf16* k, const bf16* v,             \
@@ -645,3 +698,8 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
 
 TEENY_FA2_BWD_BF16_INST(64)
 TEENY_FA2_BWD_BF16_INST(128)
+
+extern "C" __global__ __launch_bounds__(256) void teeny_fa2_dkdv_merge_bf16(
+    const float* part, bf16* dk, bf16* dv, long n, int hsplit, float scale) {
+  fa2_dkdv_merge(part, dk, dv, n, hsplit, scale);
+}

@@ -83,10 +83,16 @@ def flash_attn2_fwd(q, k, v, softmax_scale: float | None = None, causal: bool = 
     return out, lse
 
 
-def flash_attn2_bwd_workspace_bytes(q: torch.Tensor) -> int:
+def flash_attn2_bwd_workspace_bytes(q: torch.Tensor, k: torch.Tensor | None = None) -> int:
+    """Backward workspace; given k, the size that also allows the GQA head
+    split of the dK/dV kernel where it applies."""
     q4 = _as4(q)
     B, Hq, Sq, D = q4.shape
-    return _lib.lib().teeny_flash_attn2_bwd_workspace_bytes(Sq, B, Hq, D, _code(q4))
+    if k is None:
+        return _lib.lib().teeny_flash_attn2_bwd_workspace_bytes(Sq, B, Hq, D, _code(q4))
+    k4 = _as4(k)
+    return _lib.lib().teeny_flash_attn2_bwd_workspace_bytes_gqa(Sq, k4.shape[2], B, Hq, k4.shape[1],
+                                                                D, _code(q4))
 
 
 def flash_attn2_bwd(q, k, v, o, lse, do, softmax_scale: float | None = None, causal: bool = True,
@@ -97,7 +103,7 @@ def flash_attn2_bwd(q, k, v, o, lse, do, softmax_scale: float | None = None, cau
     B, Hq, Sq, D = q4.shape
     Hkv, Sk = k4.shape[1], k4.shape[2]
     scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
-    ws_bytes = flash_attn2_bwd_workspace_bytes(q4)
+    ws_bytes = flash_attn2_bwd_workspace_bytes(q4, k4)
     if workspace is None:
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
     dq = torch.empty_like(q) if dq is None else dq

@@ -52,6 +52,25 @@ def test_fa2_fwd_validation(L):
     assert fwd(L, scale=float("nan")) == VALUE
 
 
+def test_fa2_bwd_workspace_gqa(L):
+    """The larger workspace that allows the dK/dV head split: only for bf16
+    GQA with few key blocks (here 64 blocks x 8 kv heads = 512 workgroups,
+    two per CU of a 256-CU device without a GPU to ask), fp32 dK and dV
+    partials for 2 splits on top of the base workspace."""
+    f = L.teeny_flash_attn2_bwd_workspace_bytes_gqa
+    base = L.teeny_flash_attn2_bwd_workspace_bytes(8191, 1, 64, 128, BF16)
+    assert f(8191, 8191, 1, 64, 8, 128, BF16) >= base + 2 * 2 * 8 * 8191 * 128 * 4
+    # MHA, many key blocks, fp32: nothing to split
+    assert f(4096, 4096, 8, 32, 32, 128, BF16) == L.teeny_flash_attn2_bwd_workspace_bytes(
+        4096, 8, 32, 128, BF16)
+    assert f(16384, 16384, 1, 64, 8, 128, BF16) == L.teeny_flash_attn2_bwd_workspace_bytes(
+        16384, 1, 64, 128, BF16)
+    assert f(128, 128, 1, 4, 2, 64, F32) == L.teeny_flash_attn2_bwd_workspace_bytes(
+        128, 1, 4, 64, F32)
+    assert f(128, 128, 1, 6, 4, 64, BF16) == 0  # Hq % Hkv != 0
+    assert f(0, 128, 1, 4, 2, 64, BF16) == 0
+
+
 def test_fa2_bwd_workspace(L):
     need = L.teeny_flash_attn2_bwd_workspace_bytes(4096, 8, 32, 128, BF16)
     rows = 8 * 32 * 4096

@@ -159,6 +159,38 @@ def test_fa2_bf16_bwd(cuda, shape, causal):
     check_bf16("dV", host(dv), dve)
 
 
+@pytest.mark.parametrize("shape", [(2, 8, 2, 300, 300, 128), (1, 8, 1, 513, 513, 128),
+                                   (1, 16, 2, 700, 650, 64)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_fa2_bf16_bwd_gqa_split(cuda, shape, causal):
+    """dK/dV with each GQA group's q heads split over 2-4 workgroups (the
+    workspace of teeny_flash_attn2_bwd_workspace_bytes_gqa; fp32 partials
+    merged in a fixed order) and unsplit (the smaller workspace): both match
+    the oracle, dQ is the same kernel either way, and the two dK/dV differ by
+    at most the bf16 rounding of the summation order."""
+    B, Hq, Hkv, Sq, Sk, D = shape
+    q, k, v, do = inputs(50, *shape, bf16=True)
+    scale = 1.0 / math.sqrt(D)
+    qd, kd, vd, dod = (dev(t, torch.bfloat16) for t in (q, k, v, do))
+    o, lse = ops.flash_attn2_fwd(qd, kd, vd, scale, causal)
+    small = ops.flash_attn2_bwd_workspace_bytes(qd)
+    big = ops.flash_attn2_bwd_workspace_bytes(qd, kd)
+    assert big > small  # these shapes have few key blocks: the split applies
+    outs = []
+    for n in (small, big):
+        ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+        outs.append(ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod, scale, causal, workspace=ws))
+    dqe, dke, dve = O.fa2_bwd(q, k, v, host(o), do, host(lse), scale, causal)
+    for dq, dk, dv in outs:
+        check_bf16("dQ", host(dq), dqe)
+        check_bf16("dK", host(dk), dke)
+        check_bf16("dV", host(dv), dve)
+    assert torch.equal(outs[0][0], outs[1][0])
+    for a, b in ((outs[0][1], outs[1][1]), (outs[0][2], outs[1][2])):
+        a, b = host(a), host(b)
+        assert np.all(np.abs(a - b) <= np.abs(a) * 2.0 ** -7 + 1e-6)
+
+
 def test_fa2_bf16_bwd_deterministic(cuda):
     q, k, v, do = inputs(40, 1, 8, 2, 700, 700, 128, bf16=True)
     qd, kd, vd, dod = (dev(t, torch.bfloat16) for t in (q, k, v, do))
