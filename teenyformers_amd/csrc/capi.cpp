@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -245,12 +246,20 @@ size_t fa2_bwd_ws(int n_ctx_q, int batch, int hq, int head_dim, int dtype) {
   return align256((size_t)batch * hq * n_ctx_q * sizeof(float));
 }
 
-// CUs of the current device (256 on MI355X when it cannot be asked).
+// CUs of the current device, asked once per device (256, MI355X's count,
+// when it cannot be asked).  Concurrent first calls store the same value.
 int device_cus() {
-  int dev = 0, n = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev >= 0 && dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
     return 256;
+  if (dev >= 0 && dev < 64) cache[dev].store(n, std::memory_order_relaxed);
   return n;
 }
 
