@@ -256,13 +256,15 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
       mx = max3(mx, other_half(mx), mx);
       const float m_tile = mx * sl2;  // scale > 0, so max(scale*s) = scale*max(s)
       grow = __any(m_tile > m_run + kRescale);
-      const float m_new = grow ? fmaxf(m_run, m_tile) : m_run;
-      // 0 on a row's first tile; exactly 1 where the maximum is unchanged
-      alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
-      l_run2 *= alpha;
-      m_use = m_run == -INFINITY ? 0.0f : m_run;
+      if (grow) {  // wave-uniform: most tiles skip the update
+        const float m_new = fmaxf(m_run, m_tile);
+        // 0 on a row's first tile; exactly 1 where the maximum is unchanged
+        alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+        l_run2 *= alpha;
+        m_use = m_run == -INFINITY ? 0.0f : m_run;
+      }
     }
   };
   // softmax of element pair q (0..15): half q%2 (s0 / s1), rows 2(q/2), +1
