@@ -191,6 +191,39 @@ def test_fa2_bf16_bwd_gqa_split(cuda, shape, causal):
         assert np.all(np.abs(a - b) <= np.abs(a) * 2.0 ** -7 + 1e-6)
 
 
+def _random_shapes(n, seed=2026):
+    """Seeded random shapes off the tile grid: ragged lengths, Sq != Sk, GQA
+    groups 1-8, both head dims."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        hkv = int(rng.choice([1, 2, 4]))
+        group = int(rng.choice([1, 2, 4, 8]))
+        sq = int(rng.integers(1, 700))
+        sk = sq if rng.random() < 0.5 else int(rng.integers(1, 700))
+        out.append((int(rng.integers(1, 4)), hkv * group, hkv, sq, sk, int(rng.choice([64, 128])),
+                    bool(rng.random() < 0.6)))
+    return out
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Sk,D,causal", _random_shapes(12))
+def test_fa2_bf16_random_shapes(cuda, B, Hq, Hkv, Sq, Sk, D, causal):
+    """Forward and backward at seeded random shapes against the oracle."""
+    q, k, v, do = inputs(60 + Sq, B, Hq, Hkv, Sq, Sk, D, bf16=True, spike=Sk >= 100)
+    scale = 1.0 / math.sqrt(D)
+    qd, kd, vd, dod = (dev(t, torch.bfloat16) for t in (q, k, v, do))
+    o, lse = ops.flash_attn2_fwd(qd, kd, vd, scale, causal)
+    oe, le = O.fa2_fwd(q, k, v, scale, causal)
+    check_bf16("O", host(o), oe)
+    finite = np.isfinite(le)  # causal rows with no visible key (Sq > Sk) have no LSE
+    assert np.abs(host(lse)[finite] - le[finite]).max(initial=0.0) <= 2e-2
+    dq, dk, dv = ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod, scale, causal)
+    dqe, dke, dve = O.fa2_bwd(q, k, v, host(o), do, host(lse), scale, causal)
+    check_bf16("dQ", host(dq), dqe)
+    check_bf16("dK", host(dk), dke)
+    check_bf16("dV", host(dv), dve)
+
+
 def test_fa2_bf16_bwd_deterministic(cuda):
     q, k, v, do = inputs(40, 1, 8, 2, 700, 700, 128, bf16=True)
     qd, kd, vd, dod = (dev(t, torch.bfloat16) for t in (q, k, v, do))
