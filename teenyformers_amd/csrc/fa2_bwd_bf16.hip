@@ -22,10 +22,13 @@
 //      streamed into double-buffered LDS by buffer_load ... lds and read both
 //      row-wise and, through the LDS transpose read, as Q^T / dO^T),
 //      accumulating dK^T and dV^T in registers: the GQA reduction comes for
-//      free.
+//      free.  With few key blocks (long context, one sequence) the group's q
+//      heads are split over 2-4 workgroups whose fp32 partial sums a third
+//      kernel adds in a fixed order.
 // Recomputing S and dP in the dQ kernel costs 7 matrix products per tile
 // pair instead of 5; in exchange neither kernel needs dS round trips through
-// LDS, fp32 atomics or a dQ accumulator in HBM.
+// LDS, fp32 atomics or a dQ accumulator in HBM (fp32 atomic adds of that dQ
+// accumulation would cost more on MI355X than the recomputation they save).
 // Causal: blocks entirely above the diagonal are skipped, diagonal blocks
 // are masked.
 #include "cdna4.h"
