@@ -70,8 +70,8 @@ def main() -> int:
                          "Q's 256 MiB, the known-size reference for HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(attention shards over (batch, kv-head) with no exchange; see DESIGN.md)",
+        print("bench.py measures one GPU: there is no multi-GPU path (attention "
+              "would shard over (batch, kv-head) with no exchange between GPUs)",
               file=sys.stderr)
         return 2
 

@@ -1,9 +1,9 @@
 /*
  * oracle.c -- CPU restatement of teenyformers' attention hot-path kernels.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity reference for the HIP
  * library and the timed CPU baseline.  Only tests/, __graft_entry__.smoke()
- * and bench.py's cpu_baseline leg may load it, and only as the checker; the
+ * and bench.py's cpu_baseline leg may load it, and only to check results; the
  * product path (teenyformers_amd) never calls into it.
  *
  * Every function restates one reference kernel, in fp32 and in the

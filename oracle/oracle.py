@@ -1,8 +1,8 @@
 """ctypes binding of the C oracle (oracle.c) plus small numpy helpers.
 
-TEST INFRASTRUCTURE ONLY: the parity checker for the HIP library and the
+TEST INFRASTRUCTURE ONLY: the parity reference for the HIP library and the
 timed CPU baseline.  Only tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg may import this module, and only as the checker.
+cpu_baseline leg may import this module, and only to check results.
 
 All arrays are numpy, C-contiguous.  Attention tensors use the reference's
 [BH, N_CTX, HEAD_DIM] layout (src/kernels/flash_attn2.rs:23), written here as

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the parity reference.
 
 Each oracle function is checked against the reference's own golden fixtures
 (tests/golden/, copied from the reference's tests/fixtures) at the
