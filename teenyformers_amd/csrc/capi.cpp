@@ -569,6 +569,8 @@ static int norm_fwd_impl(const void* x, const void* res, void* y, void* h, float
   // Fewer rows than CUs: a workgroup per row (4 wavefronts share a row)
   // when the row is vectorised and fits 256 threads x 4 vectors.
   if (M < 256 && vec > 1 && ch <= 16) {
+    if (dtype == TEENY_BF16 && ch == 8)  // rows of 4096: 512 threads, one vector each
+      return launch("teeny_rmsnorm_fwd_wg_bf16_v8_c1_t512", dim3(M), dim3(512), 0, stream, args);
     snprintf(name, sizeof name, "teeny_rmsnorm_fwd_wg_%s_v%d_c%d", dtype_tag(dtype), vec,
              ch <= 4 ? 1 : ch / 4);
     return launch(name, dim3(M), dim3(256), 0, stream, args);
@@ -589,9 +591,11 @@ int teeny_fused_add_rmsnorm_partials_fwd(const float* parts, int n_parts, const 
   int vec, ch;
   if (!norm_shape(N, dtype, &vec, &ch) || vec == 1) return TEENY_ERR_UNSUPPORTED;
   char name[64];
+  void* args[] = {&parts, &n_parts, &residual, &y, &h, &rstd, &weight, &M, &N, &eps};
+  if (dtype == TEENY_BF16 && ch == 8)  // as the unsplit rows of 4096: 512 threads
+    return launch("teeny_addnorm_parts_fwd_bf16_v8_c1_t512", dim3(M), dim3(512), 0, stream, args);
   snprintf(name, sizeof name, "teeny_addnorm_parts_fwd_%s_v%d_c%d", dtype_tag(dtype), vec,
            ch <= 4 ? 1 : ch / 4);
-  void* args[] = {&parts, &n_parts, &residual, &y, &h, &rstd, &weight, &M, &N, &eps};
   return launch(name, dim3(M), dim3(256), 0, stream, args);
 }
 

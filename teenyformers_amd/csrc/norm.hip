@@ -201,13 +201,13 @@ extern "C" __global__ __launch_bounds__(256) void teeny_rmsnorm_dw_reduce_bf16(
 // the four wavefront sums are added in a fixed order.  PARTS: x is the sum of
 // n_parts fp32 slabs [n_parts][M][N] (a linear layer split over K), rounded
 // to T as the unsplit product would be stored.
-template <typename T, int VEC, int CH, bool PARTS = false>
+template <typename T, int VEC, int CH, bool PARTS = false, int NT = 256>
 __device__ void rmsnorm_fwd_row_wg(const T* __restrict__ x, const T* __restrict__ res,
                                    T* __restrict__ y, T* __restrict__ h_out,
                                    float* __restrict__ rstd, const T* __restrict__ w, int N,
                                    float eps, const float* __restrict__ xparts = nullptr,
                                    int n_parts = 0) {
-  __shared__ float part[kWaves];
+  __shared__ float part[NT / 64];
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
   const long base = (long)row * N;
@@ -216,7 +216,7 @@ __device__ void rmsnorm_fwd_row_wg(const T* __restrict__ x, const T* __restrict_
   float wv[CH][VEC], rv[CH][VEC];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    int idx = (c * 256 + tid) * VEC;
+    int idx = (c * NT + tid) * VEC;
     if (idx < N) {
       ldv<T, VEC>(w + idx, wv[c]);
       if (res) ldv<T, VEC>(res + base + idx, rv[c]);
@@ -228,14 +228,14 @@ __device__ void rmsnorm_fwd_row_wg(const T* __restrict__ x, const T* __restrict_
     int off[CH];            // chunks past the row re-read its first element
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const int idx = (c * 256 + tid) * VEC;
+      const int idx = (c * NT + tid) * VEC;
       off[c] = idx < N ? idx : 0;
     }
     ld_parts<T, VEC, CH>(xparts + base, (long)gridDim.x * N, n_parts, hv, off);
   }
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    int idx = (c * 256 + tid) * VEC;
+    int idx = (c * NT + tid) * VEC;
     if (idx < N) {
       if constexpr (!PARTS) ldv<T, VEC>(x + base + idx, hv[c]);
       if (res) {
@@ -254,12 +254,17 @@ __device__ void rmsnorm_fwd_row_wg(const T* __restrict__ x, const T* __restrict_
   sq = wave_sum(sq);
   if ((tid & 63) == 0) part[tid >> 6] = sq;
   __syncthreads();
-  sq = (part[0] + part[1]) + (part[2] + part[3]);
+  if constexpr (NT == 256) {
+    sq = (part[0] + part[1]) + (part[2] + part[3]);
+  } else {
+    static_assert(NT == 512, "256 or 512 threads");
+    sq = ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
+  }
   const float rs = 1.0f / sqrtf(sq * (1.0f / (float)N) + eps);
   if (tid == 0 && rstd) rstd[row] = rs;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    int idx = (c * 256 + tid) * VEC;
+    int idx = (c * NT + tid) * VEC;
     if (idx < N) {
       float out[VEC];
 #pragma unroll
@@ -293,6 +298,19 @@ TEENY_NORM_WG_INST(f32, float, 4, 4)
 TEENY_NORM_WG_INST(bf16, bf16, 8, 1)
 TEENY_NORM_WG_INST(bf16, bf16, 8, 2)
 TEENY_NORM_WG_INST(bf16, bf16, 8, 4)
+
+// 512 threads per row: bf16 rows of 4096 (one 8-element vector per thread,
+// twice the loads in flight of the 256-thread kernels)
+extern "C" __global__ __launch_bounds__(512) void teeny_rmsnorm_fwd_wg_bf16_v8_c1_t512(
+    const bf16* x, const bf16* res, bf16* y, bf16* h, float* rstd, const bf16* w, int M, int N,
+    float eps) {
+  rmsnorm_fwd_row_wg<bf16, 8, 1, false, 512>(x, res, y, h, rstd, w, N, eps);
+}
+extern "C" __global__ __launch_bounds__(512) void teeny_addnorm_parts_fwd_bf16_v8_c1_t512(
+    const float* parts, int n_parts, const bf16* res, bf16* y, bf16* h, float* rstd, const bf16* w,
+    int M, int N, float eps) {
+  rmsnorm_fwd_row_wg<bf16, 8, 1, true, 512>(nullptr, res, y, h, rstd, w, N, eps, parts, n_parts);
+}
 
 #define TEENY_NORM_INST(TN, T, VEC, CH)                                                          \
   extern "C" __global__ __launch_bounds__(256) void teeny_rmsnorm_fwd_##TN##_v##VEC##_c##CH(    \
