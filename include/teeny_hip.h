@@ -36,6 +36,16 @@ extern "C" {
 
 typedef enum { TEENY_F32 = 0, TEENY_BF16 = 1, TEENY_I32 = 2 } teeny_dtype;
 
+/* Or-ed into the dtype of a flash-attention backward (and its workspace
+ * queries): with TEENY_BF16 inputs, dq, dk and dv are fp32 gradients, as the
+ * reference's are (src/kernels/flash_attn2.rs:196-202): the kernels' fp32
+ * accumulators are stored unrounded, and P and dS enter the matrix products
+ * as two bf16 parts (hi = bf16(x), lo = bf16(x - hi)), so their operand
+ * rounding falls from 2^-9 to 2^-17 relative.  Costs two more products per
+ * tile in the dK/dV kernel and one in the dQ kernel.  No effect with
+ * TEENY_F32. */
+#define TEENY_GRAD_F32 0x100
+
 #define TEENY_OK 0
 #define TEENY_ERR_NULL_POINTER (-1)   /* a required pointer is NULL */
 #define TEENY_ERR_INVALID_SHAPE (-2)  /* a size is <= 0, inconsistent, or too large */
@@ -73,7 +83,9 @@ int teeny_profile_kernel_names(char* buf, size_t buf_bytes);
  * aligned (flash_attn2.rs:104-107).  q head h uses kv head h / (Hq / Hkv).
  * head_dim: fp32 8, 16, 32, 64, 128; bf16 64, 128.
  * neg_inf must be -INFINITY (the only value the reference passes,
- * flash_attn2.rs:478, :331).
+ * flash_attn2.rs:478, :331).  softmax_scale: finite; > 0 for bf16 (the bf16
+ * kernels fold the scale into the exponent after masking raw scores).
+ * Backward dtype: TEENY_F32, TEENY_BF16 or TEENY_BF16 | TEENY_GRAD_F32.
  * ------------------------------------------------------------------------ */
 
 /* Replaces CausalFlashAttn2RuntimeOp::pack_args + launch

@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(PKG, "libteeny_hip.so")
 HEADER = os.path.join(os.path.dirname(PKG), "include", "teeny_hip.h")
 
 TEENY_F32, TEENY_BF16, TEENY_I32 = 0, 1, 2
+TEENY_GRAD_F32 = 0x100  # or-ed into a bf16 backward's dtype: fp32 dq/dk/dv
 
 
 class TeenyError(RuntimeError):

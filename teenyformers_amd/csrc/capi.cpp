@@ -209,6 +209,15 @@ int fa2_check(const void* q, const void* k, const void* v, int n_ctx_q, int n_ct
   return TEENY_OK;
 }
 
+// The fp32 kernels take any finite scale (they scale, then mask, as the
+// reference does).  The bf16 kernels fold the scale into the exponent after
+// masking raw scores to -inf, which needs scale > 0 (-inf * 0 is NaN and a
+// negative scale would turn masked scores into +inf).
+bool scale_ok(float scale, int dtype) {
+  if (!std::isfinite(scale)) return false;
+  return dtype != TEENY_BF16 || scale > 0.0f;
+}
+
 int fa2_fwd(bool causal, const void* q, const void* k, const void* v, void* o, float* l,
             int n_ctx_q, int n_ctx_k, float scale, float neg_inf, int batch, int hq, int hkv,
             int head_dim, int dtype, hipStream_t stream) {
@@ -216,7 +225,7 @@ int fa2_fwd(bool causal, const void* q, const void* k, const void* v, void* o, f
   if (rc) return rc;
   if (!o || !l) return TEENY_ERR_NULL_POINTER;
   if (!(std::isinf(neg_inf) && neg_inf < 0)) return TEENY_ERR_INVALID_VALUE;
-  if (!std::isfinite(scale)) return TEENY_ERR_INVALID_VALUE;
+  if (!scale_ok(scale, dtype)) return TEENY_ERR_INVALID_VALUE;
   char name[64];
   const char* cz = causal ? "c" : "n";
   if (dtype == TEENY_BF16) {
@@ -289,10 +298,15 @@ int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void
             const void* dout, const float* l, void* dq, void* dk, void* dv, int n_ctx_q,
             int n_ctx_k, float scale, int batch, int hq, int hkv, int head_dim, int dtype,
             void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  // TEENY_GRAD_F32: fp32 dq/dk/dv from the bf16 kernels (the fp32 path's
+  // gradients are fp32 anyway)
+  const bool g32 = (dtype & TEENY_GRAD_F32) != 0;
+  dtype &= ~TEENY_GRAD_F32;
+  const char* gsfx = g32 && dtype == TEENY_BF16 ? "_g32" : "";
   int rc = fa2_check(q, k, v, n_ctx_q, n_ctx_k, batch, hq, hkv, head_dim, dtype);
   if (rc) return rc;
   if (!o || !dout || !l || !dq || !dk || !dv) return TEENY_ERR_NULL_POINTER;
-  if (!std::isfinite(scale)) return TEENY_ERR_INVALID_VALUE;
+  if (!scale_ok(scale, dtype)) return TEENY_ERR_INVALID_VALUE;
   if (!workspace || workspace_bytes < fa2_bwd_ws(n_ctx_q, batch, hq, head_dim, dtype))
     return TEENY_ERR_WORKSPACE;
   const long rows = (long)batch * hq * n_ctx_q;
@@ -307,7 +321,7 @@ int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void
     long total = (long)nmb * batch * hq;
     if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
     int tot = (int)total;
-    snprintf(name, sizeof name, "teeny_fa2_bwd_dq_bf16_d%d_%s", head_dim, cz);
+    snprintf(name, sizeof name, "teeny_fa2_bwd_dq_bf16_d%d_%s%s", head_dim, cz, gsfx);
     void* a2[] = {&q,       &k,       &v,     &o,  &dout, &l,   &ld,  &dq,
                   &n_ctx_q, &n_ctx_k, &scale, &hq, &hkv,  &nmb, &tot};
     rc = launch(name, dim3(tot), dim3(256), 0, stream, a2);
@@ -324,14 +338,14 @@ int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void
     total = (long)nnb * batch * hkv * hsplit;
     if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
     tot = (int)total;
-    snprintf(name, sizeof name, "teeny_fa2_bwd_dkdv_bf16_d%d_%s", head_dim, cz);
+    snprintf(name, sizeof name, "teeny_fa2_bwd_dkdv_bf16_d%d_%s%s", head_dim, cz, gsfx);
     void* a1[] = {&q,       &k,       &v,     &dout, &ld,  &dk,  &dv,  &n_ctx_q,
                   &n_ctx_k, &scale,   &hq,    &hkv,  &nnb, &tot, &hsplit, &part};
     rc = launch(name, dim3(tot), dim3(256), 0, stream, a1);
     if (rc || hsplit == 1) return rc;
     long n = (long)batch * hkv * n_ctx_k * head_dim;  // a multiple of 8
     void* a3[] = {&part, &dk, &dv, &n, &hsplit, &scale};
-    return launch("teeny_fa2_dkdv_merge_bf16", dim3((unsigned)((n / 8 + 255) / 256)), dim3(256),
+    return launch(*gsfx ? "teeny_fa2_dkdv_merge_bf16_g32" : "teeny_fa2_dkdv_merge_bf16", dim3((unsigned)((n / 8 + 255) / 256)), dim3(256),
                   0, stream, a3);
   }
   snprintf(name, sizeof name, "teeny_fa2_bwd_pre_f32_d%d", head_dim);
@@ -483,6 +497,7 @@ int teeny_flash_attn2_bwd(const void* q, const void* k, const void* v, const voi
 size_t teeny_flash_attn2_bwd_workspace_bytes(int n_ctx_q, int batch, int n_heads_q, int head_dim,
                                              int dtype) {
   if (n_ctx_q <= 0 || batch <= 0 || n_heads_q <= 0 || head_dim <= 0) return 0;
+  dtype &= ~TEENY_GRAD_F32;
   return fa2_bwd_ws(n_ctx_q, batch, n_heads_q, head_dim, dtype);
 }
 
@@ -492,6 +507,7 @@ size_t teeny_flash_attn2_bwd_workspace_bytes_gqa(int n_ctx_q, int n_ctx_k, int b
   if (n_ctx_q <= 0 || n_ctx_k <= 0 || batch <= 0 || n_heads_q <= 0 || n_heads_kv <= 0 ||
       head_dim <= 0 || n_heads_q % n_heads_kv != 0)
     return 0;
+  dtype &= ~TEENY_GRAD_F32;
   const int split = dkdv_hsplit(n_ctx_k, batch, n_heads_q, n_heads_kv, dtype);
   return fa2_bwd_ws(n_ctx_q, batch, n_heads_q, head_dim, dtype) +
          dkdv_split_bytes(n_ctx_k, batch, n_heads_kv, head_dim, split);
@@ -805,7 +821,7 @@ static int decode_attention_impl(const void* q, const void* k_cache, const void*
   if (n_heads_q / n_heads_kv > 16) return TEENY_ERR_UNSUPPORTED;
   if (head_dim < 8 || head_dim > 128 || (head_dim & (head_dim - 1)) != 0)
     return TEENY_ERR_UNSUPPORTED;
-  if (!std::isfinite(softmax_scale)) return TEENY_ERR_INVALID_VALUE;
+  if (!std::isfinite(softmax_scale) || softmax_scale <= 0.0f) return TEENY_ERR_INVALID_VALUE;
   if (!workspace ||
       workspace_bytes < teeny_decode_attention_workspace_bytes(batch, n_heads_q, n_keys, head_dim))
     return TEENY_ERR_WORKSPACE;

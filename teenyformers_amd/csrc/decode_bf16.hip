@@ -32,8 +32,8 @@ struct __attribute__((aligned(16))) DecSmem {
   char v[2][TK * D * 2];
 };
 
-// n_keys = n_keys_imm, or *n_past + 1 when n_past is given, clamped to the
-// keys the grid covers and to the cache.
+// n_keys = the n_keys argument, or min(*n_past + 1, n_keys) when n_past is
+// given (n_keys is then the grid's max_keys), clamped to the cache.
 template <int D>
 __device__ void decode_mfma(const bf16* __restrict__ q, const bf16* __restrict__ kc,
                             const bf16* __restrict__ vc, float* __restrict__ pm,
@@ -49,7 +49,7 @@ __device__ void decode_mfma(const bf16* __restrict__ q, const bf16* __restrict__
   const int split = blockIdx.x, n_split = gridDim.x;
   const int kvh = blockIdx.y, b = kvh / hkv, hk = kvh - b * hkv;
   const int group = hq / hkv;
-  if (n_past) n_keys = min(min(*n_past + 1, n_split * keys_per_split), cache_len);
+  if (n_past) n_keys = min(min(*n_past + 1, n_keys), cache_len);
   n_keys = __builtin_amdgcn_readfirstlane(n_keys);  // wave-uniform
   const int k0 = split * keys_per_split;
   const int k1 = min(k0 + keys_per_split, n_keys);
@@ -71,18 +71,21 @@ __device__ void decode_mfma(const bf16* __restrict__ q, const bf16* __restrict__
     ksrc[i] = swz<SWZ_ROW, D>(i * 64 + lane) * 16;
     vsrc[i] = swz<SWZ_DUAL, D>(i * 64 + lane) * 16;
   }
-  auto load = [&](int t0, int buf) {  // keys t0 .. t0+TK-1 (rows past the cache re-read its last)
+  // keys t0 .. t0+TK-1; rows at or past n_keys re-read row n_keys - 1: they
+  // are masked (P = 0), and a row never written (or stale, or NaN) past
+  // n_keys must not reach the P V product, where 0 * NaN would be NaN
+  auto load = [&](int t0, int buf) {
     // uniform; said explicitly, or the compiler wraps each load in a
     // per-lane loop over the values of a vector register
     const int soff = __builtin_amdgcn_readfirstlane(t0 * D * 2);
-    if (t0 + TK <= cache_len) {
+    if (t0 + TK <= n_keys) {
 #pragma unroll
       for (int i = 0; i < NLD; ++i) {
         dma16(krs, sm.k[buf] + i * 1024, ksrc[i], soff);
         dma16(vrs, sm.v[buf] + i * 1024, vsrc[i], soff);
       }
     } else {
-      const int lastrow = cache_len - 1 - t0;
+      const int lastrow = n_keys - 1 - t0;
 #pragma unroll
       for (int i = 0; i < NLD; ++i) {
         dma16(krs, sm.k[buf] + i * 1024,

@@ -41,6 +41,14 @@ constexpr int BN = 128;  // keys per workgroup
 constexpr int BM = 32;   // query rows per iteration; also the row block of the LSE / Delta array
 constexpr float kLog2e = 1.4426950408889634f;
 
+// four consecutive gradient values: bf16 (rounded to nearest even) or fp32
+__device__ inline void store4(bf16* p, float a, float b, float c, float d) {
+  *reinterpret_cast<u32x2*>(p) = u32x2{pack_bf16x2(a, b), pack_bf16x2(c, d)};
+}
+__device__ inline void store4(float* p, float a, float b, float c, float d) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{a, b, c, d};
+}
+
 
 // Per (b, q head) and block of BM query rows, ld holds BM values of
 // LSE * log2(e) followed by BM values of Delta = rowsum(O o dO), fp32; rows
@@ -61,11 +69,11 @@ struct __attribute__((aligned(16))) DkdvSmem {
 // (more workgroups when few key blocks would leave CUs idle behind the
 // heaviest causal block); each writes its fp32 dK^T, dV^T sums to
 // part[2][hsplit][B * Hkv][nk][D] (dK unscaled), merged by fa2_dkdv_merge.
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, typename GT>
 __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict__ k,
                              const bf16* __restrict__ v, const bf16* __restrict__ dout,
-                             const float* __restrict__ ld, bf16* __restrict__ dk,
-                             bf16* __restrict__ dv, int nq, int nk, float scale, int hq, int hkv,
+                             const float* __restrict__ ld, GT* __restrict__ dk,
+                             GT* __restrict__ dv, int nq, int nk, float scale, int hq, int hkv,
                              int num_n_blocks, int total_blocks, int hsplit,
                              float* __restrict__ part) {
   constexpr int DC = D / 16;            // d-chunks of 16 (QK^T, dO V^T)
@@ -75,6 +83,10 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
   constexpr int VCH = BN * CPR / 256;   // chunks per thread of the V block
   __shared__ DkdvSmem<D> sm;
 
+  // fp32 gradients: P and dS also enter the products as a second, low bf16
+  // part (x = hi + lo, hi = bf16(x), lo = bf16(x - hi)), so their bf16
+  // operand rounding (2^-9 relative) drops to 2^-17
+  constexpr bool PRECISE = std::is_same<GT, float>::value;
   const int tid = threadIdx.x;
   // wave-uniform (an SGPR): every branch on it is a scalar branch
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -270,6 +282,7 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
       constexpr int PPJ = 8 / NJ;  // dS pairs per product
       bf16x8 ta = tr_read(dt, 0, 0);
       f32x4 d4;
+      uint32_t plo[4], dslo[PRECISE ? 8 : 1];
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int hh = j / DT, t = j % DT;
@@ -277,11 +290,27 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
         if (j + 1 < NJ) tn = tr_read(dt, (j + 1) / DT, (j + 1) % DT);
         dv_acc[t] = mfma32(ta, as_bf16x8(u32x4{pb[4 * hh], pb[4 * hh + 1], pb[4 * hh + 2],
                                                  pb[4 * hh + 3]}), dv_acc[t]);
+        if constexpr (PRECISE) {
+          if (t == 0)  // the low parts of this half's P (fp32 P is still in s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              plo[i] = pack_bf16x2(s[8 * hh + 2 * i] - bf16lo(pb[4 * hh + i]),
+                                   s[8 * hh + 2 * i + 1] - bf16hi(pb[4 * hh + i]));
+          dv_acc[t] = mfma32(ta, as_bf16x8(u32x4{plo[0], plo[1], plo[2], plo[3]}), dv_acc[t]);
+        }
 #pragma unroll
         for (int i = 0; i < PPJ; ++i) {
           const int r = 2 * (j * PPJ + i);
           if ((r & 3) == 0) d4 = *reinterpret_cast<const f32x4*>(lt + BM + 8 * (r >> 2) + 4 * g);
-          dsb[r >> 1] = pack_bf16x2(s[r] * (dp[r] - d4[r & 3]), s[r + 1] * (dp[r + 1] - d4[(r & 3) + 1]));
+          if constexpr (PRECISE) {
+            const float ds0 = s[r] * (dp[r] - d4[r & 3]);
+            const float ds1 = s[r + 1] * (dp[r + 1] - d4[(r & 3) + 1]);
+            dsb[r >> 1] = pack_bf16x2(ds0, ds1);
+            dslo[r >> 1] = pack_bf16x2(ds0 - bf16lo(dsb[r >> 1]), ds1 - bf16hi(dsb[r >> 1]));
+          } else {
+            dsb[r >> 1] = pack_bf16x2(s[r] * (dp[r] - d4[r & 3]),
+                                      s[r + 1] * (dp[r + 1] - d4[(r & 3) + 1]));
+          }
         }
         if (j + 1 < NJ) ta = tn;
         __builtin_amdgcn_sched_barrier(0);
@@ -294,6 +323,9 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
         if (j + 1 < NJ) tn = tr_read(qt, (j + 1) / DT, (j + 1) % DT);
         dk_acc[t] = mfma32(ta, as_bf16x8(u32x4{dsb[4 * hh], dsb[4 * hh + 1], dsb[4 * hh + 2],
                                                   dsb[4 * hh + 3]}), dk_acc[t]);
+        if constexpr (PRECISE)
+          dk_acc[t] = mfma32(ta, as_bf16x8(u32x4{dslo[4 * hh], dslo[4 * hh + 1], dslo[4 * hh + 2],
+                                                    dslo[4 * hh + 3]}), dk_acc[t]);
         if (j + 1 < NJ) ta = tn;
       }
     }
@@ -323,27 +355,26 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
     return;
   }
   if (mykey < nk) {
-    bf16* dkr = dk + ((long)kvh * nk + mykey) * D;
-    bf16* dvr = dv + ((long)kvh * nk + mykey) * D;
+    GT* dkr = dk + ((long)kvh * nk + mykey) * D;
+    GT* dvr = dv + ((long)kvh * nk + mykey) * D;
 #pragma unroll
     for (int t = 0; t < DT; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         int d = 32 * t + 8 * j + 4 * g;
-        *reinterpret_cast<u32x2*>(dkr + d) =
-            u32x2{pack_bf16x2(dk_acc[t][4 * j] * scale, dk_acc[t][4 * j + 1] * scale),
-                  pack_bf16x2(dk_acc[t][4 * j + 2] * scale, dk_acc[t][4 * j + 3] * scale)};
-        *reinterpret_cast<u32x2*>(dvr + d) =
-            u32x2{pack_bf16x2(dv_acc[t][4 * j], dv_acc[t][4 * j + 1]),
-                  pack_bf16x2(dv_acc[t][4 * j + 2], dv_acc[t][4 * j + 3])};
+        store4(dkr + d, dk_acc[t][4 * j] * scale, dk_acc[t][4 * j + 1] * scale,
+               dk_acc[t][4 * j + 2] * scale, dk_acc[t][4 * j + 3] * scale);
+        store4(dvr + d, dv_acc[t][4 * j], dv_acc[t][4 * j + 1], dv_acc[t][4 * j + 2],
+               dv_acc[t][4 * j + 3]);
       }
   }
 }
 
 // dK = scale * sum of the hsplit partial dK^T, dV = sum of the dV^T, in
 // split order; n = B * Hkv * nk * D (a multiple of 8), 8 values per thread.
-__device__ void fa2_dkdv_merge(const float* __restrict__ part, bf16* __restrict__ dk,
-                               bf16* __restrict__ dv, long n, int hsplit, float scale) {
+template <typename GT>
+__device__ void fa2_dkdv_merge(const float* __restrict__ part, GT* __restrict__ dk,
+                               GT* __restrict__ dv, long n, int hsplit, float scale) {
   const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 8;
   if (i >= n) return;
 #pragma unroll
@@ -362,7 +393,9 @@ __device__ void fa2_dkdv_merge(const float* __restrict__ part, bf16* __restrict_
     if (w == 0)
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] *= scale;
-    Vec16<bf16>::store((w == 0 ? dk : dv) + i, acc);
+    GT* dst = (w == 0 ? dk : dv) + i;
+    store4(dst, acc[0], acc[1], acc[2], acc[3]);
+    store4(dst + 4, acc[4], acc[5], acc[6], acc[7]);
   }
 }
 
@@ -380,11 +413,11 @@ struct __attribute__((aligned(16))) DqSmem {
   char v[QVBUF][QBN * D * 2];
 };
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, typename GT>
 __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ k,
                            const bf16* __restrict__ v, const bf16* __restrict__ o,
                            const bf16* __restrict__ dout, const float* __restrict__ lse,
-                           float* __restrict__ ld, bf16* __restrict__ dq, int nq, int nk,
+                           float* __restrict__ ld, GT* __restrict__ dq, int nq, int nk,
                            float scale, int hq, int hkv, int num_m_blocks, int total_blocks) {
   constexpr int DC = D / 16;
   constexpr int DT = D / 32;
@@ -394,6 +427,9 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   constexpr int TCH = QBN * CPR / 256; // 16-byte chunks per thread per tile
   __shared__ DqSmem<D> sm;
 
+  // fp32 gradients: dS also enters the dQ product as a second, low bf16 part
+  // (dS = hi + lo), so its bf16 operand rounding drops from 2^-9 to 2^-17
+  constexpr bool PRECISE = std::is_same<GT, float>::value;
   const int tid = threadIdx.x;
   // wave-uniform (an SGPR): every branch on it is a scalar branch
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -516,8 +552,12 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
   // dS^T of the previous 32-key half (B operand of its delayed dQ^T product)
   uint32_t dsb_prev[8], dsb_new[8];
+  constexpr int NLO = PRECISE ? 8 : 1;
+  uint32_t dslo_prev[NLO], dslo_new[NLO];
 #pragma unroll
   for (int i = 0; i < 8; ++i) dsb_prev[i] = 0;
+#pragma unroll
+  for (int i = 0; i < NLO; ++i) dslo_prev[i] = 0;
 
   // S^T = K Q^T and dP^T = V dO^T for 32 keys (lane = query row, 16 keys),
   // fragments read KPF steps ahead
@@ -570,12 +610,20 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
     bf16x8 bop = as_bf16x8(
         u32x4{dsb_prev[4 * hh], dsb_prev[4 * hh + 1], dsb_prev[4 * hh + 2], dsb_prev[4 * hh + 3]});
     acc[t] = mfma32(as_bf16x8(a), bop, acc[t]);
+    if constexpr (PRECISE)
+      acc[t] = mfma32(as_bf16x8(a),
+                      as_bf16x8(u32x4{dslo_prev[4 * hh], dslo_prev[4 * hh + 1],
+                                      dslo_prev[4 * hh + 2], dslo_prev[4 * hh + 3]}),
+                      acc[t]);
   };
   // P and dS = P (dP - Delta) for score pair r, r+1 -> packed bf16
   auto ds_pair = [&](const f32x16& s, const f32x16& dp, int r) {
     const float p0 = fast_exp2(__builtin_fmaf(s[r], sl2, -lse2));
     const float p1 = fast_exp2(__builtin_fmaf(s[r + 1], sl2, -lse2));
-    dsb_new[r >> 1] = pack_bf16x2(p0 * (dp[r] - dlt), p1 * (dp[r + 1] - dlt));
+    const float ds0 = p0 * (dp[r] - dlt), ds1 = p1 * (dp[r + 1] - dlt);
+    dsb_new[r >> 1] = pack_bf16x2(ds0, ds1);
+    if constexpr (PRECISE)
+      dslo_new[r >> 1] = pack_bf16x2(ds0 - bf16lo(dsb_new[r >> 1]), ds1 - bf16hi(dsb_new[r >> 1]));
   };
   // the previous half's dQ^T product on the matrix cores, interleaved with
   // this half's exponentials on the VALU (issue order fenced)
@@ -598,6 +646,12 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
       pin(dsb_new[i]);
       dsb_prev[i] = dsb_new[i];
     }
+    if constexpr (PRECISE)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        pin(dslo_new[i]);
+        dslo_prev[i] = dslo_new[i];
+      }
   };
 
   // The first lagged product reads the K half "before" tile 0 with dS = 0:
@@ -652,57 +706,55 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   }
 
   if (qok) {
-    bf16* dqr = dq + ((long)bh * nq + qrow) * D;
+    GT* dqr = dq + ((long)bh * nq + qrow) * D;
 #pragma unroll
     for (int t = 0; t < DT; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         int d = 32 * t + 8 * j + 4 * g;
-        *reinterpret_cast<u32x2*>(dqr + d) =
-            u32x2{pack_bf16x2(acc[t][4 * j] * scale, acc[t][4 * j + 1] * scale),
-                  pack_bf16x2(acc[t][4 * j + 2] * scale, acc[t][4 * j + 3] * scale)};
+        store4(dqr + d, acc[t][4 * j] * scale, acc[t][4 * j + 1] * scale,
+               acc[t][4 * j + 2] * scale, acc[t][4 * j + 3] * scale);
       }
   }
 }
 
 }  // namespace
 
-#define TEENY_FA2_BWD_BF16_INST(D)                                                              \
+// Kernels for D in {64, 128}, causal (_c) or not (_n); GT is the gradient
+// type: bf16 (the inputs' type) or fp32 (suffix _g32, the accumulators
+// stored unrounded).
+#define TEENY_FA2_BWD_BF16_INST(D, CZ, CAUSAL, GT, SFX)                                          \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
-  void teeny_fa2_bwd_dkdv_bf16_d##D##_c(const bf16* q, const bf16* k, const bf16* v,           \
-                                        const bf16* dout, const float* ld, bf16* dk, bf16* dv,  \
-                                        int nq, int nk, float scale, int hq, int hkv, int nnb,  \
-                                        int total, int hsplit, float* part) {                   \
-    fa2_bwd_dkdv<D, true>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb, total,       \
-                          hsplit, part);                                                        \
+  void teeny_fa2_bwd_dkdv_bf16_d##D##_##CZ##SFX(                                                \
+      const bf16* q, const bf16* k, const bf16* v, const bf16* dout, const float* ld, GT* dk,   \
+      GT* dv, int nq, int nk, float scale, int hq, int hkv, int nnb, int total, int hsplit,     \
+      float* part) {                                                                            \
+    fa2_bwd_dkdv<D, CAUSAL, GT>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb, total, \
+                                hsplit, part);                                                  \
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
-  void teeny_fa2_bwd_dkdv_bf16_d##D##_n(const bf16* q, const bf16* k, const bf16* v,           \
-                                        const bf16* dout, const float* ld, bf16* dk, bf16* dv,  \
-                                        int nq, int nk, float scale, int hq, int hkv, int nnb,  \
-                                        int total, int hsplit, float* part) {                   \
-    fa2_bwd_dkdv<D, false>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb, total,      \
-                           hsplit, part);                                                       \
-  }                                                                                             \
-  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
-  void teeny_fa2_bwd_dq_bf16_d##D##_c(const bf16* q, const bf16* k, const bf16* v,             \
-                                      const bf16* o, const bf16* dout, const float* lse,        \
-                                      float* ld, bf16* dq, int nq, int nk, float scale, int hq, \
-                                      int hkv, int nmb, int total) {                            \
-    fa2_bwd_dq<D, true>(q, k, v, o, dout, lse, ld, dq, nq, nk, scale, hq, hkv, nmb, total);    \
-  }                                                                                             \
-  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
-  void teeny_fa2_bwd_dq_bf16_d##D##_n(const bf16* q, const bf16* k, const bf16* v,             \
-                                      const bf16* o, const bf16* dout, const float* lse,        \
-                                      float* ld, bf16* dq, int nq, int nk, float scale, int hq, \
-                                      int hkv, int nmb, int total) {                            \
-    fa2_bwd_dq<D, false>(q, k, v, o, dout, lse, ld, dq, nq, nk, scale, hq, hkv, nmb, total);   \
+  void teeny_fa2_bwd_dq_bf16_d##D##_##CZ##SFX(                                                  \
+      const bf16* q, const bf16* k, const bf16* v, const bf16* o, const bf16* dout,             \
+      const float* lse, float* ld, GT* dq, int nq, int nk, float scale, int hq, int hkv,        \
+      int nmb, int total) {                                                                     \
+    fa2_bwd_dq<D, CAUSAL, GT>(q, k, v, o, dout, lse, ld, dq, nq, nk, scale, hq, hkv, nmb,      \
+                              total);                                                           \
   }
 
-TEENY_FA2_BWD_BF16_INST(64)
-TEENY_FA2_BWD_BF16_INST(128)
+TEENY_FA2_BWD_BF16_INST(64, c, true, bf16, )
+TEENY_FA2_BWD_BF16_INST(64, n, false, bf16, )
+TEENY_FA2_BWD_BF16_INST(128, c, true, bf16, )
+TEENY_FA2_BWD_BF16_INST(128, n, false, bf16, )
+TEENY_FA2_BWD_BF16_INST(64, c, true, float, _g32)
+TEENY_FA2_BWD_BF16_INST(64, n, false, float, _g32)
+TEENY_FA2_BWD_BF16_INST(128, c, true, float, _g32)
+TEENY_FA2_BWD_BF16_INST(128, n, false, float, _g32)
 
 extern "C" __global__ __launch_bounds__(256) void teeny_fa2_dkdv_merge_bf16(
     const float* part, bf16* dk, bf16* dv, long n, int hsplit, float scale) {
+  fa2_dkdv_merge(part, dk, dv, n, hsplit, scale);
+}
+extern "C" __global__ __launch_bounds__(256) void teeny_fa2_dkdv_merge_bf16_g32(
+    const float* part, float* dk, float* dv, long n, int hsplit, float scale) {
   fa2_dkdv_merge(part, dk, dv, n, hsplit, scale);
 }

@@ -119,15 +119,16 @@ constexpr int kMaxD = 128;
 
 // grid (n_chunks, B * Hkv); q [B, Hq, D], caches [B, Hkv, cache_len, D].
 // Partials: m, l [B*Hq, n_chunks]; o [B*Hq, n_chunks, D] (unnormalised).
-// n_keys = n_keys_imm, or *n_past + 1 (the cached keys plus the new one)
-// when n_past is given, clamped to the keys the grid covers and the cache.
+// n_keys = the n_keys argument, or min(*n_past + 1, n_keys) (the cached keys
+// plus the new one, at most the grid's max_keys) when n_past is given,
+// clamped to the cache.
 template <typename T>
 __device__ void decode_partial(const T* __restrict__ q, const T* __restrict__ kc,
                                const T* __restrict__ vc, float* __restrict__ pm,
                                float* __restrict__ pl, float* __restrict__ po, int hq, int hkv,
                                const int* __restrict__ n_past, int n_keys, int cache_len,
                                int head_dim, float scale) {
-  if (n_past) n_keys = min(min(*n_past + 1, (int)gridDim.x * kChunk), cache_len);
+  if (n_past) n_keys = min(min(*n_past + 1, n_keys), cache_len);
   __shared__ float qs[kMaxGroup][kMaxD];
   __shared__ float ps[kMaxGroup][kChunk];
   __shared__ float red[kMaxGroup][kThreads / 64];

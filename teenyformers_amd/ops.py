@@ -96,8 +96,12 @@ def flash_attn2_bwd_workspace_bytes(q: torch.Tensor, k: torch.Tensor | None = No
 
 
 def flash_attn2_bwd(q, k, v, o, lse, do, softmax_scale: float | None = None, causal: bool = True,
-                    workspace: torch.Tensor | None = None, dq=None, dk=None, dv=None):
-    """Gradients (dq, dk, dv) of sum(O * dO); dk/dv summed over each GQA group."""
+                    workspace: torch.Tensor | None = None, dq=None, dk=None, dv=None,
+                    grad_f32: bool = False):
+    """Gradients (dq, dk, dv) of sum(O * dO); dk/dv summed over each GQA group.
+
+    grad_f32: with bf16 inputs, return fp32 gradients (the kernels' fp32
+    accumulators, unrounded; TEENY_GRAD_F32)."""
     q4, k4, v4, o4, do4 = _as4(q), _as4(k), _as4(v), _as4(o), _as4(do)
     _dev(q4, k4, v4, o4, do4, lse)
     B, Hq, Sq, D = q4.shape
@@ -106,12 +110,20 @@ def flash_attn2_bwd(q, k, v, o, lse, do, softmax_scale: float | None = None, cau
     ws_bytes = flash_attn2_bwd_workspace_bytes(q4, k4)
     if workspace is None:
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    dq = torch.empty_like(q) if dq is None else dq
-    dk = torch.empty_like(k) if dk is None else dk
-    dv = torch.empty_like(v) if dv is None else dv
+    code = _code(q4)
+    gdt = q.dtype
+    if grad_f32 and q.dtype == torch.bfloat16:
+        code |= _lib.TEENY_GRAD_F32
+        gdt = torch.float32
+    dq = torch.empty(q.shape, dtype=gdt, device=q.device) if dq is None else dq
+    dk = torch.empty(k.shape, dtype=gdt, device=q.device) if dk is None else dk
+    dv = torch.empty(v.shape, dtype=gdt, device=q.device) if dv is None else dv
+    for g in (dq, dk, dv):
+        if g.dtype != gdt or not g.is_contiguous():
+            raise ValueError(f"gradient outputs must be contiguous {gdt}")
     fn = "teeny_causal_flash_attn2_bwd" if causal else "teeny_flash_attn2_bwd"
     call(fn, _p(q4), _p(k4), _p(v4), _p(o4), _p(do4), _p(lse), _p(dq), _p(dk), _p(dv),
-         Sq, Sk, scale, B, Hq, Hkv, D, _code(q4), _p(workspace), workspace.numel(), _stream())
+         Sq, Sk, scale, B, Hq, Hkv, D, code, _p(workspace), workspace.numel(), _stream())
     return dq, dk, dv
 
 

@@ -8,6 +8,7 @@ import pytest
 from teenyformers_amd import _lib
 
 OK, NULLP, SHAPE, UNSUP, WS, VALUE = 0, -1, -2, -3, -4, -7
+GRAD_F32 = 0x100
 F32, BF16 = 0, 1
 NEG_INF = float("-inf")
 P = 0x1000  # a non-null dummy pointer: never dereferenced by failing calls
@@ -50,6 +51,34 @@ def test_fa2_fwd_validation(L):
     assert fwd(L, dtype=7) == UNSUP
     assert fwd(L, neg_inf=-1e9) == VALUE  # the reference always passes -inf
     assert fwd(L, scale=float("nan")) == VALUE
+
+
+def test_fa2_scale_domain(L):
+    """bf16 kernels fold the scale into the exponent after masking raw
+    scores to -inf: scale must be > 0 there (0 or negative would turn masked
+    scores into NaN or +inf)."""
+    assert fwd(L, scale=0.0) == VALUE
+    assert fwd(L, scale=-0.125) == VALUE
+    assert fwd(L, scale=float("inf")) == VALUE
+    ws = L.teeny_flash_attn2_bwd_workspace_bytes(128, 1, 4, 64, BF16)
+    rc = L.teeny_causal_flash_attn2_bwd(P, P, P, P, P, P, P, P, P, 128, 128, 0.0, 1, 4, 4, 64,
+                                        BF16, P, ws, None)
+    assert rc == VALUE
+    rc = L.teeny_decode_attention(P, P, P, P, 1, 4, 4, 10, 16, 64, -1.0, BF16, P, 1 << 20, None)
+    assert rc == VALUE
+
+
+def test_fa2_grad_f32_flag(L):
+    """TEENY_GRAD_F32 changes the gradients' type, not the workspace."""
+    for args in ((4096, 8, 32, 128), (300, 2, 8, 128), (128, 1, 4, 64)):
+        assert L.teeny_flash_attn2_bwd_workspace_bytes(*args, BF16 | GRAD_F32) == \
+            L.teeny_flash_attn2_bwd_workspace_bytes(*args, BF16)
+    f = L.teeny_flash_attn2_bwd_workspace_bytes_gqa
+    assert f(8191, 8191, 1, 64, 8, 128, BF16 | GRAD_F32) == f(8191, 8191, 1, 64, 8, 128, BF16)
+    # validation still applies to the flagged dtype
+    rc = L.teeny_causal_flash_attn2_bwd(P, P, P, P, P, P, P, P, P, 128, 128, 0.125, 1, 4, 4, 32,
+                                        BF16 | GRAD_F32, P, 1 << 20, None)
+    assert rc == UNSUP
 
 
 def test_fa2_bwd_workspace_gqa(L):

@@ -82,6 +82,16 @@ def test_rope_bf16(cuda, bh, s, d):
     assert bf16_close(got, want)
 
 
+@pytest.mark.parametrize("bh,s,d", [(32, 2048, 64), (8, 1000, 128), (2, 16384, 128)])
+def test_rope_bf16_bwd(cuda, bh, s, d):
+    """rope_backward (src/kernels/rope.rs:104-140) on bf16 gradients: within
+    one bf16 rounding of the oracle on the same rounded input."""
+    dy = O.bf16_round(randn(17, bh, s, d))
+    want = O.rope(dy, f32_ln(5e5), backward=True)
+    got = host(ops.rope(dev(dy, torch.bfloat16), 5e5, backward=True))
+    assert bf16_close(got, want)
+
+
 # ---------------------------------------------------------------------------
 # Head transposes (bit-exact)
 # ---------------------------------------------------------------------------
@@ -153,6 +163,37 @@ def test_rmsnorm_bf16(cuda, m, n):
     assert np.all(err <= np.abs(y2) * 2.0 ** -7 + 1e-2 * 2.0 ** -7)
 
 
+def bf16_grad_close(got, want):
+    """A bf16 gradient against the oracle's fp32 one on the same rounded
+    inputs: one bf16 rounding, plus 1e-5 of the tensor's scale for the fp32
+    row sums (dot(dy, w h), the weight gradient's sum over rows) that the
+    kernel and the oracle add in different orders."""
+    return np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -8 + 1e-5 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("m,n", [(8192, 2048), (100, 4096), (3, 1000)])
+def test_rmsnorm_bf16_bwd(cuda, m, n):
+    """bf16 backward of the fused add+RMSNorm (the reference's formula,
+    src/kernels/fused_add_rmsnorm.rs:128-190) and of the plain norm (true
+    gradient), rstd from the GPU forward as the backward receives it."""
+    h = O.bf16_round(randn(18, m, n))
+    w = O.bf16_round(1 + 0.1 * randn(19, n))
+    g = O.bf16_round(randn(20, m, n))
+    hd, wd, gd = dev(h, torch.bfloat16), dev(w, torch.bfloat16), dev(g, torch.bfloat16)
+    _, rstd = ops.rmsnorm(hd, wd, 1e-5)
+    r = host(rstd)
+    assert np.abs(r - O.rmsnorm_fwd(h, w, 1e-5)[1]).max() <= 1e-5 * np.abs(r).max()
+    dx, dres, dw = ops.fused_add_rmsnorm_bwd(gd, hd, wd, rstd)
+    dxe, _, dwe = O.fused_add_rmsnorm_bwd(g, h, w, r)
+    assert bf16_grad_close(host(dx), dxe)
+    assert torch.equal(dx, dres)
+    assert bf16_grad_close(host(dw), dwe)
+    dxp, dwp = ops.rmsnorm_bwd(gd, hd, wd, rstd)
+    dxpe, dwpe = O.rmsnorm_bwd(g, h, w, r)
+    assert bf16_grad_close(host(dxp), dxpe)
+    assert bf16_grad_close(host(dwp), dwpe)
+
+
 # ---------------------------------------------------------------------------
 # SwiGLU
 # ---------------------------------------------------------------------------
@@ -174,6 +215,16 @@ def test_swiglu_bf16(cuda):
     z = O.bf16_round(randn(14, 2048, 2 * 8192))
     got = host(ops.swiglu(dev(z, torch.bfloat16)))
     assert bf16_close(got, O.swiglu_fwd(z))
+
+
+@pytest.mark.parametrize("m,f", [(2048, 8192), (33, 100)])
+def test_swiglu_bf16_bwd(cuda, m, f):
+    """swiglu_backward (src/kernels/swiglu.rs:97-136) on bf16: dz within one
+    bf16 rounding of the oracle on the same rounded inputs."""
+    z = O.bf16_round(randn(21, m, 2 * f))
+    g = O.bf16_round(randn(22, m, f))
+    got = host(ops.swiglu_bwd(dev(g, torch.bfloat16), dev(z, torch.bfloat16)))
+    assert bf16_close(got, O.swiglu_bwd(g, z))
 
 
 # ---------------------------------------------------------------------------

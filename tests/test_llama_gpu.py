@@ -77,6 +77,40 @@ def test_decode_attention(cuda, dtype, n_keys, L, D, Hq, Hkv):
         assert rel_l2(host(o), want) <= 5e-3 and np.abs(host(o) - want).max() <= 2e-2
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n_keys,L,D,Hq,Hkv", [(300, 768, 128, 32, 8), (45, 64, 64, 8, 2),
+                                               (1001, 1100, 128, 16, 1)])
+def test_decode_attention_ignores_rows_past_n_keys(cuda, dtype, n_keys, L, D, Hq, Hkv):
+    """Cache rows at or past n_keys (never written, or stale) may hold
+    anything, NaN included: the output depends only on rows below n_keys.
+    Host-position and device-position calls, n_keys off the 32-key tile; and
+    the device-position call attends min(n_past + 1, max_keys) rows."""
+    B = 2
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q = torch.randn((B, Hq, D), generator=g, device="cuda").to(dtype)
+    kc = torch.randn((B, Hkv, L, D), generator=g, device="cuda").to(dtype)
+    vc = torch.randn((B, Hkv, L, D), generator=g, device="cuda").to(dtype)
+    kc[:, :, n_keys:] = float("nan")
+    vc[:, :, n_keys:] = float("nan")
+    scale = 1.0 / math.sqrt(D)
+    want, _ = O.fa2_fwd(host(q)[:, :, None], host(kc[:, :, :n_keys]), host(vc[:, :, :n_keys]),
+                        scale, causal=False)
+    want = want[:, :, 0]
+    pdev = torch.tensor([n_keys - 1], dtype=torch.int32, device="cuda")
+    for o in (ops.decode_attention(q, kc, vc, n_keys, scale),
+              ops.decode_attention(q, kc, vc, L, scale, n_past=pdev)):
+        got = host(o)
+        assert np.isfinite(got).all()
+        if dtype == torch.float32:
+            assert np.abs(got - want).max() <= 1e-5
+        else:
+            assert rel_l2(got, want) <= 5e-3 and np.abs(got - want).max() <= 2e-2
+    # max_keys below n_past + 1 caps the rows attended
+    cap = n_keys - 7
+    o_cap = ops.decode_attention(q, kc, vc, cap, scale, n_past=pdev)
+    assert torch.equal(o_cap, ops.decode_attention(q, kc, vc, cap, scale))
+
+
 def _oracle_block(cfg, w, x):
     """One LlamaBlock from the oracle's restated ops + float32 numpy GEMMs."""
     B, S, d = x.shape
