@@ -54,6 +54,7 @@ typedef enum { TEENY_F32 = 0, TEENY_BF16 = 1, TEENY_I32 = 2 } teeny_dtype;
 #define TEENY_ERR_HIP (-5)            /* a HIP runtime call failed (teeny_last_hip_error) */
 #define TEENY_ERR_MODULE (-6)         /* code object or kernel symbol could not be loaded */
 #define TEENY_ERR_INVALID_VALUE (-7)  /* a scalar argument is out of its domain */
+#define TEENY_ERR_SCRATCH (-8)        /* needs more than the static scratch array (noalloc) */
 
 /* Library version, error text, last HIP error seen by this thread. */
 int teeny_abi_version(void);
@@ -139,6 +140,25 @@ size_t teeny_flash_attn2_bwd_workspace_bytes(int n_ctx_q, int batch, int n_heads
 size_t teeny_flash_attn2_bwd_workspace_bytes_gqa(int n_ctx_q, int n_ctx_k, int batch,
                                                  int n_heads_q, int n_heads_kv, int head_dim,
                                                  int dtype);
+
+/* No counterpart in the reference: teeny_causal_flash_attn2_bwd for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc).  The workspace is a static device
+ * array of this library, teeny_scratch_bytes() (16 MiB) per device, held until
+ * the process ends; its address is looked up once per device (teeny_init or
+ * the first call).  Problems whose teeny_flash_attn2_bwd_workspace_bytes
+ * exceed it return TEENY_ERR_SCRATCH (B*Hq*ceil32(n_ctx_q)*8 bytes for bf16:
+ * e.g. B8 Hq32 S4096 needs 8 MiB).  A GQA split runs when it fits in the
+ * array.  Calls no allocating routine.  Every call on a device shares that
+ * device's array: calls that overlap on one device (other streams or
+ * threads) race.  Arguments otherwise as teeny_causal_flash_attn2_bwd. */
+size_t teeny_scratch_bytes(void);
+int teeny_causal_flash_attn2_bwd_noalloc(const void* q, const void* k, const void* v,
+                                         const void* o, const void* dout, const float* l,
+                                         void* dq, void* dk, void* dv, int n_ctx_q, int n_ctx_k,
+                                         float softmax_scale, int batch, int n_heads_q,
+                                         int n_heads_kv, int head_dim, int dtype,
+                                         hipStream_t stream);
 
 /* --------------------------------------------------------------------------
  * RoPE on x [BH, n_ctx, head_dim], interleaved pairs, position = row index.

@@ -48,6 +48,8 @@ _SIGNATURES = {
     "teeny_causal_flash_attn2_bwd": ([_p] * 9 + [_i, _i, _f, _i, _i, _i, _i, _i, _p, _sz, _p], _i),
     "teeny_flash_attn2_bwd": ([_p] * 9 + [_i, _i, _f, _i, _i, _i, _i, _i, _p, _sz, _p], _i),
     "teeny_flash_attn2_bwd_workspace_bytes": ([_i, _i, _i, _i, _i], _sz),
+    "teeny_scratch_bytes": ([], _sz),
+    "teeny_causal_flash_attn2_bwd_noalloc": ([_p] * 9 + [_i, _i, _f, _i, _i, _i, _i, _i, _p], _i),
     "teeny_flash_attn2_bwd_workspace_bytes_gqa": ([_i] * 7, _sz),
     "teeny_rope_fwd": ([_p, _p, _i, _f, _i, _i, _i, _p], _i),
     "teeny_rope_bwd": ([_p, _p, _i, _f, _i, _i, _i, _p], _i),

@@ -6,8 +6,12 @@ Steps:
   1. each csrc/*.hip -> _build/<name>.hsaco with `hipcc --genco` for gfx950
      (in parallel);
   2. the code objects are embedded into an assembler blob (.incbin);
-  3. csrc/capi.cpp + the blob -> teenyformers_amd/libteeny_hip.so (g++ against
-     the HIP runtime; the host library has no device code of its own).
+  3. csrc/noalloc.hip -> _build/noalloc.o with `hipcc -c -fPIC` (host code
+     plus a device part that holds only the no-allocation entry point's
+     static scratch array, registered with the HIP runtime when the library
+     loads);
+  4. csrc/capi.cpp + the blob + noalloc.o -> teenyformers_amd/libteeny_hip.so
+     (g++ against the HIP runtime).
 
 Every HIP file is compiled with packed-fp32 instruction selection disabled
 (-packed-fp32-ops): the kernels' fp32 math is issued as scalar VALU ops; and
@@ -92,12 +96,18 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     blob_o = os.path.join(BUILD, "co_blob.o")
     _run(["gcc", "-c", blob, "-o", blob_o], verbose)
 
+    noalloc_o = os.path.join(BUILD, "noalloc.o")
+    _run([os.path.join(ROCM, "bin", "hipcc"), "-O2", "-std=c++17", f"--offload-arch={ARCH}",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-fPIC",
+          f"-I{INCLUDE}", "-c", os.path.join(CSRC, "noalloc.hip"),
+          "-o", noalloc_o], verbose)
+
     tmp = LIB + ".tmp"
     cmd = [
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared",
         "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE}", f"-I{ROCM}/include",
         "-Wall", "-Wextra", "-Wno-unused-parameter",
-        os.path.join(CSRC, "capi.cpp"), blob_o,
+        os.path.join(CSRC, "capi.cpp"), blob_o, noalloc_o,
         f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
         "-o", tmp,
     ]

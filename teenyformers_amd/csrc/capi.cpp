@@ -37,6 +37,9 @@
   X(decode_bf16)         \
   X(linear_bf16)
 
+// noalloc.hip: the current device's address of its static scratch array
+extern "C" __attribute__((visibility("hidden"))) int teeny_scratch_setup(void** out);
+
 #define TEENY_CO_DECL(n) \
   extern "C" const unsigned char teeny_co_##n[]; \
   extern "C" const unsigned char teeny_co_##n##_end[];
@@ -406,6 +409,7 @@ const char* teeny_strerror(int code) {
     case TEENY_ERR_HIP: return "HIP runtime error";
     case TEENY_ERR_MODULE: return "code object or kernel could not be loaded";
     case TEENY_ERR_INVALID_VALUE: return "invalid scalar argument";
+    case TEENY_ERR_SCRATCH: return "problem needs more than the library's static scratch array";
     default: return "unknown error";
   }
 }
@@ -415,10 +419,20 @@ int teeny_init(void) {
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e);
   if (dev < 0 || dev >= kMaxDevices) return TEENY_ERR_HIP;
-  std::lock_guard<std::mutex> lk(g_mu);
-  DeviceState* st = nullptr;
-  return load_device_locked(dev, &st);
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    DeviceState* st = nullptr;
+    int rc = load_device_locked(dev, &st);
+    if (rc) return rc;
+  }
+  // this device's address of the no-allocation entry point's scratch array;
+  // a failure here is reported by that entry point (it asks again), not by
+  // the rest of the library
+  (void)teeny_scratch_setup(nullptr);
+  return TEENY_OK;
 }
+
+__attribute__((visibility("hidden"))) void teeny_set_last_hip_error(int e) { g_last_hip = e; }
 
 int teeny_profile_enable(int on) {
   std::lock_guard<std::mutex> lk(g_prof_mu);

@@ -7,7 +7,7 @@ import pytest
 
 from teenyformers_amd import _lib
 
-OK, NULLP, SHAPE, UNSUP, WS, VALUE = 0, -1, -2, -3, -4, -7
+OK, NULLP, SHAPE, UNSUP, WS, VALUE, SCRATCH = 0, -1, -2, -3, -4, -7, -8
 GRAD_F32 = 0x100
 F32, BF16 = 0, 1
 NEG_INF = float("-inf")
@@ -79,6 +79,19 @@ def test_fa2_grad_f32_flag(L):
     rc = L.teeny_causal_flash_attn2_bwd(P, P, P, P, P, P, P, P, P, 128, 128, 0.125, 1, 4, 4, 32,
                                         BF16 | GRAD_F32, P, 1 << 20, None)
     assert rc == UNSUP
+
+
+def test_noalloc_bwd_refuses_beyond_scratch(L):
+    """The no-allocation backward's static array is 16 MiB per device;
+    problems whose workspace exceeds it are refused before anything runs."""
+    assert L.teeny_scratch_bytes() == 16 << 20
+    # B8 Hq32 S4096 D128 needs 8 MiB: within; B8 Hq32 S16384 needs 32 MiB
+    assert L.teeny_flash_attn2_bwd_workspace_bytes(4096, 8, 32, 128, BF16) <= 16 << 20
+    assert L.teeny_flash_attn2_bwd_workspace_bytes(16384, 8, 32, 128, BF16) > 16 << 20
+    rc = L.teeny_causal_flash_attn2_bwd_noalloc(P, P, P, P, P, P, P, P, P, 16384, 16384, 0.088,
+                                                8, 32, 32, 128, BF16, None)
+    assert rc == SCRATCH
+    assert "scratch" in L.teeny_strerror(SCRATCH).decode()
 
 
 def test_fa2_bwd_workspace_gqa(L):
