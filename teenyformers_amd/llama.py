@@ -222,10 +222,15 @@ class Llama:
         f = ops.linear_swiglu(n2, self.w[p + "gate_up_proj.weight"])
         return ops.linear_split(f, self.w[p + "down_proj.weight"])
 
-    def hidden(self, ids: torch.Tensor, cache: KVCache, pos0) -> torch.Tensor:
+    def hidden(self, ids: torch.Tensor, cache: KVCache, pos0, trace: list | None = None
+               ) -> torch.Tensor:
         """Final-norm hidden states [B, S, d] for ids [B, S] at positions pos0..,
         appending the new keys/values to `cache` (pos0 may be an int32 device
-        tensor for one-token steps; cache.length is then left to the caller)."""
+        tensor for one-token steps; cache.length is then left to the caller).
+        trace: if a list, each block appends (x, attn, x + attn, ffn): its
+        input residual stream, the attention sub-layer's output, the stream
+        after the attention add, and the FFN output (the block's output is
+        the sum of the last two)."""
         cfg, w = self.cfg, self.w
         x = ops.token_embed(ids.to(torch.int32).contiguous(), w["model.embed_tokens.weight"])
         eps = cfg.eps
@@ -236,9 +241,12 @@ class Llama:
                 n1, _ = ops.rmsnorm(x, w[p + "input_layernorm.weight"], eps, want_rstd=False)
             else:  # x = x + ffn(...) fused into this block's input norm
                 n1, x, _ = ops.fused_add_rmsnorm(delta, x, w[p + "input_layernorm.weight"], eps)
+            x_in = x
             a = self._attention(i, n1, cache, pos0)
             n2, x, _ = ops.fused_add_rmsnorm(a, x, w[p + "post_attention_layernorm.weight"], eps)
             delta = self._ffn(i, n2)
+            if trace is not None:
+                trace.append((x_in, a, x, delta))
         y, _, _ = ops.fused_add_rmsnorm(delta, x, w["model.norm.weight"], eps)
         if not isinstance(pos0, torch.Tensor):
             cache.length = pos0 + ids.shape[1]
