@@ -14,7 +14,8 @@ are resident in HBM before timing.  Prints one JSON line:
               sample of heads on this host's cores
   detail      per-op numbers (forward, backward, each kernel), plus the other
               configurations: long-context GQA FA2 (B1 Hq64 Hkv8 D128,
-              S=16384 and the ragged 8191, 1% of K rows x8), one Llama block
+              S=16384 and the ragged 8191, 1% of K rows x8), the library's
+              GEMM at the Llama prompt shapes beside hipBLASLt, one Llama block
               forward (B4 S2048 d2048, Hq32/Hkv8, F8192, bf16), and the
               Llama-3-8B-shaped model (32 layers, d4096, Hq32/Hkv8, F14336,
               vocab 128256, random N(0, 0.02) bf16 weights): prefill of 16 x 512
@@ -61,7 +62,7 @@ def main() -> int:
                     help="skip the long-context GQA, Llama block and Llama-8B measurements")
     ap.add_argument("--no-power", action="store_true",
                     help="skip the power / clock sampling phase")
-    ap.add_argument("--only", choices=["bandwidth", "block", "gqa", "llama8b"],
+    ap.add_argument("--only", choices=["bandwidth", "block", "gqa", "llama8b", "gemm"],
                     help="run only one of the secondary measurements (one JSON line): the "
                          "HBM-bound kernels at the Llama-block shapes, one Llama block, the "
                          "long-context GQA FA2, or the Llama-8B-shape prefill + decode")
@@ -86,7 +87,8 @@ def main() -> int:
         run = {"bandwidth": ("bandwidth_c2", lambda: bench_bandwidth(torch, ops, _lib)),
                "block": ("llama_block", lambda: bench_llama_block(torch)),
                "gqa": ("fa2_gqa_long", lambda: bench_gqa_long(torch, ops)),
-               "llama8b": ("llama_8b_shape", lambda: bench_llama_8b(torch))}[args.only]
+               "llama8b": ("llama_8b_shape", lambda: bench_llama_8b(torch)),
+               "gemm": ("gemm", lambda: bench_gemm(torch))}[args.only]
         print(json.dumps({run[0]: run[1]()}), flush=True)
         return 0
     gen = torch.Generator(device=dev).manual_seed(1234)
@@ -186,6 +188,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         out["detail"]["bandwidth_c2"] = bench_bandwidth(torch, ops, _lib)
         out["detail"]["fa2_gqa_long"] = bench_gqa_long(torch, ops)
+        out["detail"]["gemm"] = bench_gemm(torch)
         out["detail"]["llama_block"] = bench_llama_block(torch)
         out["detail"]["llama_8b_shape"] = bench_llama_8b(torch)
         torch.cuda.empty_cache()
@@ -248,7 +251,9 @@ def bench_gqa_long(torch, ops):
 def bench_bandwidth(torch, ops, lib, reps: int = 20):
     """The HBM-bound kernels at the Llama-block shapes (B4 S2048, d2048, Hq32
     Hkv8 D64, F8192, bf16): RoPE, head transposes, RMSNorm, residual-add
-    RMSNorm, SwiGLU.  Duration per call = HIP events (on the launch stream)
+    RMSNorm, SwiGLU; and the head transpose and RoPE at the attention
+    benchmark's [8, 4096, 32, 128] (256 MiB), each beside a device copy of
+    the same bytes.  Duration per call = HIP events (on the launch stream)
     around one replay of a graph of `reps` calls, / reps; bytes are the
     algorithmic reads + writes.  A torch device copy of Q's bytes is the
     size's practical ceiling."""
@@ -278,6 +283,16 @@ def bench_bandwidth(torch, ops, lib, reps: int = 20):
     ]
     qc = torch.empty_like(q)
     cases.append(("torch copy of Q's bytes (reference)", lambda: qc.copy_(q), 2 * q.numel() * 2))
+    # the attention benchmark's size: [8, 4096, 32, 128] bf16, 256 MiB a tensor
+    xl = rnd(8, 4096, 32 * 128)
+    ql = xl.view(8 * 32, 4096, 128)
+    qlo, xlc = torch.empty_like(ql), torch.empty_like(xl)
+    cases += [
+        ("transpose_heads [8,4096,32*128]", lambda: ops.transpose_heads(xl, 32),
+         2 * xl.numel() * 2),
+        ("rope_fwd [256,4096,128]", lambda: ops.rope(ql, 5e5, out=qlo), 2 * ql.numel() * 2),
+        ("torch copy of 256 MiB (reference)", lambda: xlc.copy_(xl), 2 * xl.numel() * 2),
+    ]
     res = {}
     for name, fn, nbytes in cases:
         lib.profile_enable(True)  # one call recorded: which kernels it launches
@@ -307,6 +322,36 @@ def bench_bandwidth(torch, ops, lib, reps: int = 20):
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "gbs": round(gbs, 1),
                      "pct_hbm_peak": round(gbs / PEAK_HBM_GBS, 4), "kernels": kernels}
+    return res
+
+
+def bench_gemm(torch, reps: int = 20):
+    """The library's bf16 GEMM (teeny_linear_bf16, y = x W^T) at the prompt
+    shapes of the Llama-3-8B shape (16 x 512 tokens) and the Llama block
+    (4 x 2048 tokens), next to torch's GEMM (hipBLASLt) on the same operands."""
+    from teenyformers_amd import ops
+
+    shapes = {"8b qkv": (8192, 6144, 4096), "8b o": (8192, 4096, 4096),
+              "8b gate_up": (8192, 28672, 4096), "8b down": (8192, 4096, 14336),
+              "block qkv": (8192, 3072, 2048), "block o": (8192, 2048, 2048),
+              "block gate_up": (8192, 16384, 2048), "block down": (8192, 2048, 8192)}
+    res = {}
+    for name, (M, N, K) in shapes.items():
+        x = torch.randn((M, K), device="cuda").to(torch.bfloat16)
+        w = (0.02 * torch.randn((N, K), device="cuda")).to(torch.bfloat16)
+        y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+
+        def lib_gemm():
+            ops.call("teeny_linear_bf16", ops._p(x), ops._p(w), ops._p(y), M, N, K, ops._stream())
+
+        ms = _time(torch, lib_gemm, reps)
+        ms_t = _time(torch, lambda: torch.nn.functional.linear(x, w), reps)
+        f = 2.0 * M * N * K
+        res[name] = {"M": M, "N": N, "K": K, "ms": round(ms, 4),
+                     "tflops": round(f / ms / 1e9, 1), "pct_peak": round(f / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+                     "hipblaslt_tflops": round(f / ms_t / 1e9, 1),
+                     "vs_hipblaslt": round(ms_t / ms, 3)}
+        del x, w, y
     return res
 
 

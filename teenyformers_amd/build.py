@@ -15,7 +15,7 @@ Steps:
 
 Every HIP file is compiled with packed-fp32 instruction selection disabled
 (-packed-fp32-ops): the kernels' fp32 math is issued as scalar VALU ops; and
-with MFMA operands in VGPR form (see HIPCC_FLAGS).
+all but the GEMM with MFMA accumulators in VGPR form (see VGPR_FORM).
 """
 from __future__ import annotations
 
@@ -37,19 +37,21 @@ ARCH = "gfx950"
 # Order matters only for readability; capi.cpp declares the same list.
 KERNEL_SOURCES = [
     "transpose", "rope", "norm", "swiglu", "embed", "fa2_f32", "fa2_fwd_bf16", "fa2_bwd_bf16",
-    "llama", "decode_bf16", "linear_bf16",
+    "llama", "decode_bf16", "linear_bf16", "gemm_bf16",
 ]
 
 HIPCC_FLAGS = [
     "-O3", "-std=c++17", f"--offload-arch={ARCH}", "--genco",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-munsafe-fp-atomics", "-ffp-contract=fast",
-    # keep MFMA accumulators in the VGPR file: with AGPR accumulators the
-    # loop-carried dK/dV sums were copied between register files every
-    # iteration
-    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wno-unused-result",
 ]
+# keep MFMA accumulators in the VGPR file: with AGPR accumulators the
+# loop-carried dK/dV sums were copied between register files every
+# iteration.  The GEMM keeps them in AGPRs (its accumulators are read only
+# once, at the end, and a wavefront's 128 x 128 tile needs all 256).
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+NO_VGPR_FORM = {"gemm_bf16"}
 
 
 def _run(cmd, verbose):
@@ -73,7 +75,8 @@ EXTRA_FLAGS: dict[str, list[str]] = {}
 def _hipcc(name, verbose):
     src = os.path.join(CSRC, name + ".hip")
     out = os.path.join(BUILD, name + ".hsaco")
-    cmd = [os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, *EXTRA_FLAGS.get(name, []),
+    vf = [] if name in NO_VGPR_FORM else VGPR_FORM
+    cmd = [os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, *vf, *EXTRA_FLAGS.get(name, []),
            "-I", CSRC, src, "-o", out]
     _run(cmd, verbose)
     return out

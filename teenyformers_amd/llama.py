@@ -21,8 +21,8 @@ MI355X-specific structure (same arithmetic):
   * prefill runs the causal FA2 kernel over the cache; each decode step runs
     teeny_decode_attention over the cached keys;
   * Linear layers (teeny-core's external `Linear`, src/layers/mod.rs:54-58,
-    y = x W^T with W [out, in]) are hipBLASLt GEMMs through torch for a
-    prompt; with at most 16 rows (a decode step) they are this library's
+    y = x W^T with W [out, in]) are this library's kernels: the matrix-core
+    GEMM for a prompt, and with at most 16 rows (a decode step) the
     weight-streaming kernels: gate_up fused with SwiGLU, and q|k|v, o and
     down split over K into fp32 slabs that the QKV split and the
     residual-add norms sum.

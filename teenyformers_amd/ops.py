@@ -435,24 +435,36 @@ def argmax_rows(x, out=None):
     return out
 
 
+def _no_grad(x2: torch.Tensor, w: torch.Tensor) -> bool:
+    # the library's linear kernels have no backward: autograd uses torch's GEMM
+    return not (torch.is_grad_enabled() and (x2.requires_grad or w.requires_grad))
+
+
 def _skinny(x2: torch.Tensor, w: torch.Tensor, n_out: int, row_tile: int = 128) -> bool:
-    """Shapes the decode-step linear kernels take (else a general GEMM runs)."""
+    """Shapes the decode-step linear kernels take."""
     M, K = x2.shape
-    if torch.is_grad_enabled() and (x2.requires_grad or w.requires_grad):
-        return False  # the kernels have no backward
-    return (x2.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x2.is_cuda
-            and 1 <= M <= 16 and K % 128 == 0 and n_out % row_tile == 0 and w.is_contiguous())
+    return (_no_grad(x2, w) and x2.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+            and x2.is_cuda and 1 <= M <= 16 and K % 128 == 0 and n_out % row_tile == 0
+            and w.is_contiguous())
+
+
+def _gemm(x2: torch.Tensor, w: torch.Tensor) -> bool:
+    """Shapes teeny_linear_bf16 takes (any M; N and K multiples of 64)."""
+    N, K = w.shape
+    return (_no_grad(x2, w) and x2.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+            and x2.is_cuda and N % 64 == 0 and K % 64 == 0 and w.is_contiguous())
 
 
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """y = x w^T (src/layers/mod.rs:54-58; w [out, in]).  Up to 16 rows of
-    bf16 run the weight-streaming decode kernel; larger M is a GEMM for the
-    matrix-core GEMM library (hipBLASLt through torch)."""
+    """y = x w^T (src/layers/mod.rs:54-58; w [out, in]) through teeny_linear_bf16:
+    up to 16 rows of bf16 stream the weight (decode kernels), more rows run
+    the library's matrix-core GEMM.  fp32 (the reference's precision, used
+    by the parity tests) and products that need a gradient use torch's GEMM."""
     x2 = x.reshape(-1, x.shape[-1])
     N, K = w.shape
     if K != x2.shape[1]:
         raise ValueError(f"linear: x has {x2.shape[1]} features, w expects {K}")
-    if not _skinny(x2, w, N):
+    if not _gemm(x2, w):
         return torch.nn.functional.linear(x, w)
     x2 = x2.contiguous()
     y = torch.empty((x2.shape[0], N), dtype=x.dtype, device=x.device)
@@ -469,7 +481,7 @@ def linear_swiglu(x: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
         raise ValueError("linear_swiglu: weight must be [2F, in] with in = x's features")
     F = N2 // 2
     if not _skinny(x2, w_gate_up, F, row_tile=64):
-        return swiglu(torch.nn.functional.linear(x, w_gate_up))
+        return swiglu(linear(x, w_gate_up))
     x2 = x2.contiguous()
     y = torch.empty((x2.shape[0], F), dtype=x.dtype, device=x.device)
     call("teeny_linear_swiglu_bf16", _p(x2), _p(w_gate_up), _p(y), x2.shape[0], F, K, _stream())
@@ -513,7 +525,7 @@ def linear_split(x: torch.Tensor, w: torch.Tensor, k_split: int | None = None):
     if K != x2.shape[1]:
         raise ValueError(f"linear: x has {x2.shape[1]} features, w expects {K}")
     if not _skinny(x2, w, N):
-        return torch.nn.functional.linear(x, w)
+        return linear(x, w)
     x2 = x2.contiguous()
     ks = _k_split(K, N) if k_split is None else k_split
     n = _lib.lib().teeny_linear_partials_count(K, ks)

@@ -141,10 +141,13 @@ def test_other_ops_validation(L):
 
 
 def test_decode_ops_validation(L):
-    # decode-step linears: M <= 16, N % 128 (F % 64), K % 128
-    assert L.teeny_linear_bf16(P, P, P, 17, 128, 128, None) == UNSUP
-    assert L.teeny_linear_bf16(P, P, P, 16, 64, 128, None) == UNSUP
-    assert L.teeny_linear_bf16(P, P, P, 16, 128, 96, None) == UNSUP
+    # linear: any M; the matrix-core GEMM needs N % 64 and K % 64 (the
+    # decode-step kernels, M <= 16, N % 128 and K % 128)
+    assert L.teeny_linear_bf16(P, P, P, 17, 96, 128, None) == UNSUP
+    assert L.teeny_linear_bf16(P, P, P, 16, 64, 96, None) == UNSUP
+    assert L.teeny_linear_bf16(P, P, P, 300, 128, 4100, None) == UNSUP
+    assert L.teeny_linear_bf16(P, P, P, 300, 128, 1 << 22, None) == SHAPE  # 32-bit offsets
+    assert L.teeny_linear_swiglu_bf16(P, P, P, 17, 64, 128, None) == UNSUP
     assert L.teeny_linear_bf16(None, P, P, 16, 128, 128, None) == NULLP
     assert L.teeny_linear_bf16(P, P, P, 0, 128, 128, None) == SHAPE
     assert L.teeny_linear_swiglu_bf16(P, P, P, 4, 32, 128, None) == UNSUP

@@ -340,10 +340,3 @@ def test_linear_swiglu_skinny(cuda, M, F, K):
     # one bf16 step of z can move silu(g) * u by a few output ulps
     assert np.all(err <= np.abs(want) * 2.0 ** -5 + 1e-3 * np.abs(want).max()), err.max()
     assert rel_l2(host(y), want) <= 5e-3
-
-
-def test_linear_large_m_uses_gemm(cuda):
-    """More than 16 rows is a general GEMM (same product, torch's library)."""
-    x = torch.randn((17, 256), device="cuda", dtype=torch.bfloat16)
-    w = torch.randn((32, 256), device="cuda", dtype=torch.bfloat16)
-    assert torch.equal(ops.linear(x, w), torch.nn.functional.linear(x, w))
