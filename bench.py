@@ -478,9 +478,15 @@ def traffic_from_profiles(kernel: str):
 
 
 def cpu_baseline(q, k, v, do, scale, n_heads):
-    """Time the oracle (fp32 restatement of the reference kernels, every key of
-    every query row like the reference's loop) on n_heads (b, h) slices of the
-    same inputs, and report TFLOP/s with the same algorithmic FLOP count."""
+    """The oracle (the build's fp32 C restatement of the reference kernels,
+    OpenMP over rows) on this host's cores.  value: the attention step's
+    fwd+bwd (every key of every query row, as the reference loops) timed on
+    n_heads of the 256 (b, h) heads and extrapolated linearly to all of them,
+    in the same algorithmic TFLOP/s as the GPU line.  legs: the reference's
+    CPU path on the other configurations, in full: the fp32 FA2 forward with
+    RoPE and head transpose at B1 H4 S128 D64, and RoPE, head transpose,
+    RMSNorm, residual-add RMSNorm and SwiGLU at the Llama-block shapes (fp32,
+    the oracle's precision; GB/s over the fp32 bytes each moves)."""
     import numpy as np
 
     from oracle import oracle as O
@@ -496,26 +502,112 @@ def cpu_baseline(q, k, v, do, scale, n_heads):
     t2 = time.perf_counter()
     f_fwd = fwd_flops(1, n_heads, S, S, D)
     f_tot = 3.5 * f_fwd
+    legs = cpu_legs(np, O)
     return {
         "value": round(f_tot / (t2 - t0) / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"fwd+bwd of {n_heads} of the {B * H} (b, h) heads at S={S}, D={D}, fp32; "
-                  f"fwd {t1 - t0:.2f} s, bwd {t2 - t1:.2f} s",
-        "cpu": _cpu_model(),
+        "sample": f"fwd+bwd of {n_heads} of the {B * H} (b, h) heads at S={S}, D={D}, fp32, "
+                  f"extrapolated to all {B * H} (linear in heads); fwd {t1 - t0:.2f} s, "
+                  f"bwd {t2 - t1:.2f} s",
+        "extrapolated": True,
+        "host": _host(threads),
+        "legs": legs,
     }
 
 
-def _cpu_model():
+def cpu_legs(np, O):
+    """The oracle on the other configurations, each in full (fp32)."""
+    rng = np.random.default_rng(5)
+
+    def rnd(*shape):
+        return rng.standard_normal(shape, dtype=np.float32)
+
+    def timed(fn, reps=3):
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        return (time.perf_counter() - t0) / reps
+
+    legs = {}
+    # FA2 forward, fp32, B1 H4 S128 D64: RoPE (theta 1e4) on Q and K, head
+    # transpose [B,S,H,D] -> [B,H,S,D], causal attention
+    Bc, Sc, Hc, Dc = 1, 128, 4, 64
+    xq, xk, xv = rnd(Bc, Sc, Hc * Dc), rnd(Bc, Sc, Hc * Dc), rnd(Bc, Sc, Hc * Dc)
+    lnb = float(np.log(np.float32(1e4)).astype(np.float32))
+
+    def c1():
+        qh = O.rope(O.transpose_heads(xq, Bc, Sc, Hc, Dc), lnb)
+        kh = O.rope(O.transpose_heads(xk, Bc, Sc, Hc, Dc), lnb)
+        vh = O.transpose_heads(xv, Bc, Sc, Hc, Dc)
+        O.fa2_fwd(qh, kh, vh, 1.0 / math.sqrt(Dc), True, all_keys=True)
+
+    sec = timed(c1, reps=20)
+    f = fwd_flops(Bc, Hc, Sc, Sc, Dc)
+    legs["fa2_fwd_rope_transpose B1 H4 S128 D64"] = {
+        "ms": round(sec * 1e3, 3), "tflops_attention": round(f / sec / 1e12, 6)}
+    # the Llama-block shapes (B4 S2048, d2048, Hq32 Hkv8 D64, F8192)
+    M, dm, F = 4 * 2048, 2048, 8192
+    qb = rnd(4 * 32, 2048, 64)
+    xb = rnd(4, 2048, 32 * 64)
+    x, r, w = rnd(M, dm), rnd(M, dm), rnd(dm)
+    z = rnd(M, 2 * F)
+    lnb5 = float(np.log(np.float32(5e5)).astype(np.float32))
+    cases = [
+        ("rope_fwd Q [128,2048,64]", lambda: O.rope(qb, lnb5), 2 * qb.size * 4),
+        ("transpose_heads Q [4,2048,32*64]", lambda: O.transpose_heads(xb, 4, 2048, 32, 64),
+         2 * xb.size * 4),
+        ("rmsnorm [8192,2048]", lambda: O.rmsnorm_fwd(x, w, 1e-5), 2 * M * dm * 4),
+        ("fused_add_rmsnorm [8192,2048]", lambda: O.fused_add_rmsnorm_fwd(x, r, w, 1e-5),
+         4 * M * dm * 4),
+        ("swiglu_fwd [8192,2*8192]", lambda: O.swiglu_fwd(z), 3 * M * F * 4),
+    ]
+    for name, fn, nbytes in cases:
+        sec = timed(fn)
+        legs[name] = {"ms": round(sec * 1e3, 3), "gbs": round(nbytes / sec / 1e9, 2)}
+    return legs
+
+
+def _host(threads):
+    """This host: CPU model, logical CPUs, the CPUs this process may use."""
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = None
+    return {"cpu": _cpu_model(), "nproc": os.cpu_count(), "usable_cpus": usable,
+            "oracle_threads": threads}
+
+
+def _cpu_model():
+    """The CPU model string: lscpu's "Model name" (with its vendor and family
+    fields when the name alone is generic), else /proc/cpuinfo."""
+    import subprocess
+
+    fields = {}
+    try:
+        r = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10)
+        for line in r.stdout.splitlines():
+            if ":" in line:
+                key, val = line.split(":", 1)
+                fields[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
-    return "unknown"
+    name = fields.get("Model name")
+    if not name:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        name = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+    extra = [f"{k} {fields[k]}" for k in ("Vendor ID", "CPU family", "Model", "Socket(s)",
+                                          "Core(s) per socket", "Thread(s) per core")
+             if k in fields]
+    return "; ".join([name or "unknown"] + extra)
 
 
 if __name__ == "__main__":

@@ -164,7 +164,8 @@ int teeny_causal_flash_attn2_bwd_noalloc(const void* q, const void* k, const voi
  * RoPE on x [BH, n_ctx, head_dim], interleaved pairs, position = row index.
  * Replaces RopeRtOp::pack_args (src/kernels/rope.rs:180-204): (x, y, n_ctx,
  * ln_rope_base) and pack_backward_args (:210-237): (dy, dx, n_ctx,
- * ln_rope_base).  head_dim even; a multiple of 4 (fp32) or 8 (bf16).
+ * ln_rope_base).  head_dim: a power of two (the reference requires it,
+ * rope.rs:56), at least 4 (fp32) or 8 (bf16).
  * In-place (y == x) is allowed.
  * ------------------------------------------------------------------------ */
 int teeny_rope_fwd(const void* x, void* y, int n_ctx, float ln_rope_base, int bh, int head_dim,
@@ -231,9 +232,14 @@ int teeny_swiglu_fwd(const void* z, void* out, int M, int d_ff, int dtype, hipSt
 int teeny_swiglu_bwd(const void* grad, const void* z, void* dz, int M, int d_ff, int dtype,
                      hipStream_t stream);
 
+/* Elementwise residual add y = a + b over n values (a, b, y 16-byte
+ * aligned; y may alias a or b).  Replaces the Op::Add that sym_add records
+ * (src/layers/mod.rs:36-48), which the reference lowers through teeny-core. */
+int teeny_add(const void* a, const void* b, void* y, long n, int dtype, hipStream_t stream);
+
 /* --------------------------------------------------------------------------
  * Token embedding gather: out[s, :] = weight[ids[s], :].
- * Replaces TokenEmbedRuntimeOp::pack_args (src/layers/embedding.rs:56-72):
+ * Replaces TokenEmbedRuntimeOp::pack_args (src/layers/embedding.rs:65-80):
  *   (ids, weight, out, seq_len, d_model).  ids_dtype TEENY_F32 (the
  *   reference's encoding, src/kernels/token_embed.rs:32) or TEENY_I32; an id
  *   outside [0, vocab_size) gives a zero row.

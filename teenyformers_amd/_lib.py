@@ -62,6 +62,7 @@ _SIGNATURES = {
     "teeny_rmsnorm_bwd": ([_p] * 6 + [_i, _i, _i, _p, _sz, _p], _i),
     "teeny_swiglu_fwd": ([_p, _p, _i, _i, _i, _p], _i),
     "teeny_swiglu_bwd": ([_p, _p, _p, _i, _i, _i, _p], _i),
+    "teeny_add": ([_p, _p, _p, ctypes.c_long, _i, _p], _i),
     "teeny_token_embed_fwd": ([_p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "teeny_qkv_rope_split": ([_p] * 4 + [_i] * 7 + [_f, _i, _p], _i),
     "teeny_decode_attention_workspace_bytes": ([_i] * 4, _sz),

@@ -716,6 +716,19 @@ int teeny_swiglu_bwd(const void* grad, const void* z, void* dz, int M, int d_ff,
   return swiglu_impl(true, grad, z, dz, M, d_ff, dtype, stream);
 }
 
+int teeny_add(const void* a, const void* b, void* y, long n, int dtype, hipStream_t stream) {
+  if (!a || !b || !y) return TEENY_ERR_NULL_POINTER;
+  if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
+  if (n <= 0 || n >= (1L << 40)) return TEENY_ERR_INVALID_SHAPE;
+  // whole 16-byte vectors: every pointer 16-byte aligned
+  if (((uintptr_t)a | (uintptr_t)b | (uintptr_t)y) % 16 != 0) return TEENY_ERR_INVALID_VALUE;
+  char name[32];
+  snprintf(name, sizeof name, "teeny_add_%s", dtype_tag(dtype));
+  void* args[] = {&a, &b, &y, &n};
+  const long blocks = (n + 8L * 256 - 1) / (8L * 256);
+  return launch(name, dim3((unsigned)blocks), dim3(256), 0, stream, args);
+}
+
 static int qkv_rope_split_check(const void* qkv, const void* q_out, const void* k_cache,
                                 const void* v_cache, int batch, int seq_len, int pos0,
                                 int cache_len, int n_heads_q, int n_heads_kv, int head_dim,

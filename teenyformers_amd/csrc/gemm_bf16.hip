@@ -28,8 +28,9 @@
 // column: the ~32 workgroups resident on an XCD share 4 x-row tiles and 8
 // w-row tiles.
 //
-// Rows past M or N re-read the last row (their outputs are not stored);
-// K must be a multiple of 64 and N of 64 (checked by the host).
+// Rows past M or N lie outside the operands' buffer ranges and load as
+// zeros (their outputs are not stored); K must be a multiple of 64 and N of
+// 64 (checked by the host).
 #include "cdna4.h"
 
 #include <numeric>
@@ -113,24 +114,29 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
   const int m0 = tm * GBM, n0 = tn * GBN;
 
   // ---- DMA sources: slot P = j * NT + tid (16 bytes) of a tile holds the
-  //      chunk of row r = P / CPR whose position gpos gives ------------------
+  //      chunk of row r = P / CPR whose position gpos gives.  Load j of a
+  //      thread is its load 0 shifted by j * NT / CPR rows (a multiple of 32,
+  //      which keeps the swizzle), so only that row offset changes, and it
+  //      is uniform.  Rows past M or N fall outside the buffer range: the
+  //      loads return zeros (no access), and they only feed outputs that
+  //      are not stored. ---------------------------------------------------
+  static_assert((NT / CPR) % 32 == 0, "row step of the DMA loads keeps the swizzle");
   const int rows_x = min(GBM, M - m0), rows_w = min(GBN, N - n0);
   const auto xr = make_rsrc(x + (long)m0 * K, rows_x * K * 2);
   const auto wr = make_rsrc(w + (long)n0 * K, rows_w * K * 2);
-  uint32_t xsrc[LPT], wsrc[LPT];
-#pragma unroll
-  for (int j = 0; j < LPT; ++j) {
-    const int P = j * NT + tid, r = P / CPR;
-    const int c = (gpos<BK>(r, P % CPR) - r * BK * 2) >> 4;  // the swizzle is an involution
-    xsrc[j] = (uint32_t)(min(r, rows_x - 1) * K * 2 + c * 16);
-    wsrc[j] = (uint32_t)(min(r, rows_w - 1) * K * 2 + c * 16);
+  uint32_t src0;
+  {
+    const int r = tid / CPR;
+    const int c = (gpos<BK>(r, tid % CPR) - r * BK * 2) >> 4;  // the swizzle is an involution
+    src0 = (uint32_t)(r * K * 2 + c * 16);
   }
+  const int jstride = (NT / CPR) * K * 2;  // bytes between load j and j + 1
   auto load = [&](int kt, int buf) {
     const int soff = __builtin_amdgcn_readfirstlane(kt * BK * 2);
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
-      dma16(xr, smx[buf] + j * NT * 16 + wave * 1024, xsrc[j], soff);
-      dma16(wr, smw[buf] + j * NT * 16 + wave * 1024, wsrc[j], soff);
+      dma16(xr, smx[buf] + j * NT * 16 + wave * 1024, src0, soff + j * jstride);
+      dma16(wr, smw[buf] + j * NT * 16 + wave * 1024, src0, soff + j * jstride);
     }
   };
 

@@ -66,7 +66,41 @@ __device__ void swiglu_bwd(const T* __restrict__ grad, const T* __restrict__ z,
   stv<T, VEC>(dz + zoff + F, du);
 }
 
+// Elementwise residual add y = a + b over n values (the reference's sym_add,
+// src/layers/mod.rs:36-48, Op::Add): 8 consecutive values per thread as
+// 16-byte (bf16) or two 16-byte (fp32) vectors; n % 8 values at the end one
+// at a time.
+template <typename T>
+__device__ void add_kernel(const T* __restrict__ a, const T* __restrict__ b, T* __restrict__ y,
+                           long n) {
+  const long i = ((long)blockIdx.x * kThreads + threadIdx.x) * 8;
+  if (i + 8 <= n) {
+    float va[8], vb[8];
+    constexpr int N = Vec16<T>::N;
+#pragma unroll
+    for (int h = 0; h < 8; h += N) {
+      Vec16<T>::load(a + i + h, va + h);
+      Vec16<T>::load(b + i + h, vb + h);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) va[j] += vb[j];
+#pragma unroll
+    for (int h = 0; h < 8; h += N) Vec16<T>::store(y + i + h, va + h);
+  } else {
+    for (long j = i; j < n; ++j) st(y + j, ld(a + j) + ld(b + j));
+  }
+}
+
 }  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void teeny_add_f32(const float* a, const float* b,
+                                                                float* y, long n) {
+  add_kernel<float>(a, b, y, n);
+}
+extern "C" __global__ __launch_bounds__(256) void teeny_add_bf16(const bf16* a, const bf16* b,
+                                                                 bf16* y, long n) {
+  add_kernel<bf16>(a, b, y, n);
+}
 
 #define TEENY_SWIGLU_INST(TN, T, VEC)                                                      \
   extern "C" __global__ __launch_bounds__(256) void teeny_swiglu_fwd_##TN##_v##VEC(       \

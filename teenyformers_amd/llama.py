@@ -326,7 +326,7 @@ def block_forward(cfg: LlamaConfig, w: dict, x: torch.Tensor, layer: int = 0) ->
     a = model._attention(layer, n1, cache, 0)
     n2, x2, _ = ops.fused_add_rmsnorm(a, x, w[p + "post_attention_layernorm.weight"], cfg.eps)
     f = model._ffn(layer, n2)
-    return x2 + f
+    return ops.add(x2, f)
 
 
 def prefill_flops(cfg: LlamaConfig, batch: int, seq: int, last_logits_only: bool = True) -> float:

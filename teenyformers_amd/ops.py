@@ -328,6 +328,16 @@ def swiglu_bwd(grad: torch.Tensor, z: torch.Tensor) -> torch.Tensor:
     return dz
 
 
+def add(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """a + b (the residual add, src/layers/mod.rs:36-48)."""
+    _dev(a, b)
+    if a.shape != b.shape or a.dtype != b.dtype or not (a.is_contiguous() and b.is_contiguous()):
+        raise ValueError("add: a and b must be contiguous tensors of one shape and dtype")
+    out = torch.empty_like(a) if out is None else out
+    call("teeny_add", _p(a), _p(b), _p(out), a.numel(), _code(a), _stream())
+    return out
+
+
 class SwigluFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, z):

@@ -140,6 +140,13 @@ def test_other_ops_validation(L):
     assert L.teeny_token_embed_fwd(P, P, P, 4, 16, 10, BF16, F32, None) == UNSUP  # ids dtype
 
 
+def test_add_validation(L):
+    assert L.teeny_add(None, P, P, 16, BF16, None) == NULLP
+    assert L.teeny_add(P, P, P, 0, BF16, None) == SHAPE
+    assert L.teeny_add(P + 2, P, P, 16, BF16, None) == VALUE  # not 16-byte aligned
+    assert L.teeny_add(P, P, P, 16, 9, None) == UNSUP
+
+
 def test_decode_ops_validation(L):
     # linear: any M; the matrix-core GEMM needs N % 64 and K % 64 (the
     # decode-step kernels, M <= 16, N % 128 and K % 128)

@@ -242,3 +242,17 @@ def test_token_embed(cuda, dtype):
     assert torch.equal(got_f, want) and torch.equal(got_i, want)
     bad = ops.token_embed(torch.tensor([-1, V, 3], dtype=torch.int32, device="cuda"), w)
     assert torch.equal(bad[0], torch.zeros_like(bad[0])) and torch.equal(bad[2], w[3])
+
+
+# ---------------------------------------------------------------------------
+# Residual add (bit-exact: one fp32 add of the stored values, rounded once)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n", [8192 * 2048, 1001, 8])
+def test_residual_add(cuda, dtype, n):
+    a = dev(randn(23, n), dtype)
+    b = dev(randn(24, n), dtype)
+    want = (a.float() + b.float()).to(dtype)  # exact fp32 sum of two bf16/fp32 values, rounded
+    assert torch.equal(ops.add(a, b), want)
+    assert torch.equal(ops.add(a, b, out=a), want)  # in place
