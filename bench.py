@@ -287,6 +287,14 @@ def bench_bandwidth(torch, ops, lib, reps: int = 20):
     xl = rnd(8, 4096, 32 * 128)
     ql = xl.view(8 * 32, 4096, 128)
     qlo, xlc = torch.empty_like(ql), torch.empty_like(xl)
+    # the Llama-3-8B-shape prefill's fused QKV split + RoPE + cache write
+    qkv8 = rnd(16, 512, 48 * 128)
+    q8 = torch.empty((16, 32, 512, 128), dtype=torch.bfloat16, device="cuda")
+    kc8 = torch.empty((16, 8, 640, 128), dtype=torch.bfloat16, device="cuda")
+    vc8 = torch.empty_like(kc8)
+    cases.append(("qkv_rope_split [16,512,(32+2*8)*128]",
+                  lambda: ops.qkv_rope_split(qkv8, q8, kc8, vc8, 0, 32, 8, 5e5),
+                  2 * qkv8.numel() * 2))
     cases += [
         ("transpose_heads [8,4096,32*128]", lambda: ops.transpose_heads(xl, 32),
          2 * xl.numel() * 2),

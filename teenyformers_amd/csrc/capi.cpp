@@ -743,7 +743,10 @@ static int qkv_rope_split_check(const void* qkv, const void* q_out, const void* 
   const int vn = dtype == TEENY_BF16 ? 8 : 4;
   if (head_dim % vn != 0 || head_dim % 2 != 0) return TEENY_ERR_UNSUPPORTED;
   if (!std::isfinite(ln_rope_base)) return TEENY_ERR_INVALID_VALUE;
-  if ((long)batch * ((n_heads_q + 2 * n_heads_kv + 15) / 16) > 65535)
+  // row kernel: one thread per 16-byte vector of a head row, 8 head rows each
+  if (head_dim / vn > 256) return TEENY_ERR_UNSUPPORTED;
+  if ((long)batch * ((n_heads_q + 2 * n_heads_kv + 7) / 8) > 65535 ||
+      (long)batch * ((n_heads_q + 2 * n_heads_kv + 3) / 4) > 65535)
     return TEENY_ERR_INVALID_SHAPE;
   return TEENY_OK;
 }
@@ -756,14 +759,14 @@ static int qkv_rope_split_impl(const void* qkv, void* q_out, void* k_cache, void
                                 n_heads_q, n_heads_kv, head_dim, ln_rope_base, dtype);
   if (rc) return rc;
   const int htot = n_heads_q + 2 * n_heads_kv;
-  const long gy = (long)batch * ((htot + 15) / 16);
-  if (gy > 65535) return TEENY_ERR_INVALID_SHAPE;
+  // 256 threads: (256 / vectors per row) positions x 8 head rows each
+  const long gy = (long)batch * ((htot + 7) / 8);
+  const int ppw = 256 / (head_dim / (dtype == TEENY_BF16 ? 8 : 4));
   char name[48];
   snprintf(name, sizeof name, "teeny_qkv_rope_split_%s", dtype_tag(dtype));
   void* args[] = {&qkv,      &q_out,     &k_cache,   &v_cache,    &seq_len,   &pos_dev,
                   &pos0,     &cache_len, &n_heads_q, &n_heads_kv, &head_dim,  &ln_rope_base};
-  unsigned shmem = 16u * (unsigned)(head_dim / 2) * 8u;
-  return launch(name, dim3((seq_len + 15) / 16, (unsigned)gy), dim3(256), shmem, stream, args);
+  return launch(name, dim3((seq_len + ppw - 1) / ppw, (unsigned)gy), dim3(256), 0, stream, args);
 }
 
 int teeny_qkv_rope_split(const void* qkv, void* q_out, void* k_cache, void* v_cache, int batch,

@@ -21,9 +21,9 @@
 namespace {
 
 constexpr int kThreads = 256;
-// A workgroup covers kRows head rows (of Hq + 2 Hkv) x kPos positions: 16 x 16
-// for a prompt; 4 x 4 for the few rows of a decode step, whose QKV comes as
-// K-split slabs, so that 12x more workgroups share the slab reads.
+// The slab form (decode steps, whose QKV comes as K-split slabs): a
+// workgroup covers 4 head rows (of Hq + 2 Hkv) x 4 positions with a (cos,
+// sin) table in LDS, so that many workgroups share the slab reads.
 
 // PARTS: qkv is the sum of n_parts fp32 slabs part_stride apart (the QKV
 // projection split over K), rounded to T as the unsplit product is stored.
@@ -105,6 +105,77 @@ __device__ void qkv_rope_split(const T* __restrict__ qkv, T* __restrict__ q_out,
     } else {
 #pragma unroll
       for (int j = 0; j < VN; ++j) out[j] = in[j];
+    }
+    Vec16<T>::store(dst + v * VN, out);
+  }
+}
+
+// The prompt form: a thread owns one 16-byte vector column (position s,
+// pairs v*VN/2 ..) of kQkvHeads consecutive head rows of a qkv row.  It
+// issues those loads first, evaluates its VN/2 (cos, sin) pairs while they
+// are in flight, then rotates (q and k heads) or copies (v heads) and stores
+// them: no LDS table, no barrier, the transcendental work amortised over the
+// heads (the standalone RoPE kernel's layout).  Consecutive threads take
+// consecutive vectors of a row, then consecutive positions, so every load
+// and store is a run of whole rows.
+constexpr int kQkvHeads = 8;
+
+template <typename T>
+__device__ void qkv_rope_rows(const T* __restrict__ qkv, T* __restrict__ q_out,
+                              T* __restrict__ k_cache, T* __restrict__ v_cache, int seq,
+                              const int* __restrict__ pos_dev, int pos0, int cache_len, int hq,
+                              int hkv, int head_dim, float ln_base) {
+  constexpr int VN = Vec16<T>::N;
+  const int vpr = head_dim / VN;  // vectors per head row (the host keeps it <= kThreads)
+  const int ppw = kThreads / vpr;
+  const int v = threadIdx.x % vpr;
+  const int s = blockIdx.x * ppw + threadIdx.x / vpr;
+  const int htot = hq + 2 * hkv;
+  const int groups = (htot + kQkvHeads - 1) / kQkvHeads;
+  const int b = blockIdx.y / groups;
+  const int h0 = (blockIdx.y - b * groups) * kQkvHeads;
+  if (s >= seq || (int)threadIdx.x >= ppw * vpr) return;
+  const T* src = qkv + (((long)b * seq + s) * htot + h0) * head_dim + v * VN;
+  float in[kQkvHeads][VN];
+#pragma unroll
+  for (int h = 0; h < kQkvHeads; ++h)
+    if (h0 + h < htot) Vec16<T>::load(src + (long)h * head_dim, in[h]);
+
+  if (pos_dev) pos0 += *pos_dev;
+  const int pos = pos0 + s;
+  float cn[VN / 2], sn[VN / 2];
+  if (h0 < hq + hkv) {  // some head of the group is rotated
+    const float c = (-2.0f * ln_base) / (float)head_dim;
+#pragma unroll
+    for (int j = 0; j < VN / 2; ++j) {
+      const int k = v * (VN / 2) + j;
+      const float inv = (float)exp((double)((float)k * c));
+      sincosf((float)pos * inv, &sn[j], &cn[j]);
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < kQkvHeads; ++h) {
+    const int hh = h0 + h;
+    if (hh >= htot) break;
+    if (hh >= hq && (pos < 0 || pos >= cache_len)) continue;  // outside the cache
+    T* dst;
+    if (hh < hq)
+      dst = q_out + (((long)b * hq + hh) * seq + s) * head_dim;
+    else if (hh < hq + hkv)
+      dst = k_cache + (((long)b * hkv + (hh - hq)) * cache_len + pos) * head_dim;
+    else
+      dst = v_cache + (((long)b * hkv + (hh - hq - hkv)) * cache_len + pos) * head_dim;
+    float out[VN];
+    if (hh < hq + hkv) {
+#pragma unroll
+      for (int j = 0; j < VN / 2; ++j) {
+        const float x0 = in[h][2 * j], x1 = in[h][2 * j + 1];
+        out[2 * j] = x0 * cn[j] - x1 * sn[j];
+        out[2 * j + 1] = x0 * sn[j] + x1 * cn[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < VN; ++j) out[j] = in[h][j];
     }
     Vec16<T>::store(dst + v * VN, out);
   }
@@ -374,8 +445,8 @@ TEENY_QKV_PARTS_INST(bf16, bf16)
   extern "C" __global__ __launch_bounds__(256) void teeny_qkv_rope_split_##TN(                 \
       const T* qkv, T* q_out, T* k_cache, T* v_cache, int seq, const int* pos_dev, int pos0,    \
       int cache_len, int hq, int hkv, int head_dim, float ln_base) {                            \
-    qkv_rope_split<T>(qkv, q_out, k_cache, v_cache, seq, pos_dev, pos0, cache_len, hq, hkv,     \
-                      head_dim, ln_base);                                                       \
+    qkv_rope_rows<T>(qkv, q_out, k_cache, v_cache, seq, pos_dev, pos0, cache_len, hq, hkv,      \
+                     head_dim, ln_base);                                                        \
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(256) void teeny_decode_attn_partial_##TN(            \
       const T* q, const T* kc, const T* vc, float* pm, float* pl, float* po, int hq, int hkv,   \
