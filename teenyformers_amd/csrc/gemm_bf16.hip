@@ -49,6 +49,12 @@ constexpr int kVmWaitLgkm0() {
   return kVmWait<n>() & ~(15 << 8);
 }
 
+// s_barrier alone: __syncthreads() also waits for every memory operation in
+// flight (vmcnt(0)), which would wait for the tiles loading further ahead;
+// the caller waits for exactly what the barrier publishes.  The memory
+// clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
 // f(integral_constant<T>) for T = B .. E-1
 template <int B, int E, typename F>
 __device__ __forceinline__ void unroll_tiles(F&& f) {
@@ -60,7 +66,6 @@ __device__ __forceinline__ void unroll_tiles(F&& f) {
 
 namespace {
 
-constexpr int GBM = 256, GBN = 256;
 
 // LDS byte offset of 16-byte chunk c of tile row r (rows of BK bf16):
 // BK = 64: 128-byte rows, two per line, c ^= (r >> 1) & 7;
@@ -71,27 +76,29 @@ DEVI int gpos(int r, int c) {
   else return r * 64 + ((c ^ ((r >> 2) & 3)) << 4);
 }
 
-// BK: K per LDS tile; NS: tiles in flight (LDS buffers); WAVES: wavefronts
-// per workgroup, WGM of them along M (WAVES / WGM along N); GROUP_M:
-// tile-rows per group of the tile order; RA: 16-k steps of fragment
-// read-ahead.
-template <int BK, int NS, int WAVES, int WGM, int GROUP_M, int RA>
+// BM x BN: the workgroup's tile of y; BK: K per LDS tile; NS: tiles in
+// flight (LDS buffers); WAVES: wavefronts per workgroup, WGM of them along M
+// (WAVES / WGM along N); GROUP_M: tile-rows per group of the tile order; RA:
+// 16-k steps of fragment read-ahead.
+template <int BM, int BN, int BK, int NS, int WAVES, int WGM, int GROUP_M, int RA>
 __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const bf16* __restrict__ w,
                              bf16* __restrict__ y, int M, int N, int K, int tiles_m,
                              int tiles_n) {
-  constexpr int TILEB = GBM * BK * 2;          // bytes per operand tile
+  constexpr int XTILE = BM * BK * 2, WTILE = BN * BK * 2;  // bytes per operand tile
   constexpr int NT = 64 * WAVES;                // threads
-  constexpr int LPT = TILEB / (NT * 16);       // 16-byte DMA loads per thread per operand tile
-  constexpr int STEPS = BK / 16;               // 16-k steps per tile
+  constexpr int LPX = XTILE / (NT * 16);        // 16-byte DMA loads per thread, x tile
+  constexpr int LPW = WTILE / (NT * 16);        // ... w tile
+  constexpr int STEPS = BK / 16;                // 16-k steps per tile
+  static_assert(RA <= STEPS, "fragments are read at most one tile ahead");
   constexpr int WGN = WAVES / WGM;
-  constexpr int WM = GBM / WGM, WN = GBN / WGN;  // wavefront tile
+  constexpr int WM = BM / WGM, WN = BN / WGN;   // wavefront tile
   constexpr int I = WM / 32, J = WN / 32;        // 32 x 32 blocks per wavefront
   constexpr int CPR = BK / 8;                    // 16-byte chunks per row
   // one LDS object: with the x and w tiles in separate __shared__ arrays the
   // compiler waited for every LDS DMA in flight before each fragment read
   struct __attribute__((aligned(16))) Smem {
-    char x[NS][TILEB];
-    char w[NS][TILEB];
+    char x[NS][XTILE];
+    char w[NS][WTILE];
   };
   __shared__ Smem sm;
   auto& smx = sm.x;
@@ -111,7 +118,7 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
   const int gm = min(tiles_m - first_m, GROUP_M);
   const int in_grp = id - grp * per_group;
   const int tm = first_m + in_grp % gm, tn = in_grp / gm;
-  const int m0 = tm * GBM, n0 = tn * GBN;
+  const int m0 = tm * BM, n0 = tn * BN;
 
   // ---- DMA sources: slot P = j * NT + tid (16 bytes) of a tile holds the
   //      chunk of row r = P / CPR whose position gpos gives.  Load j of a
@@ -121,7 +128,7 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
   //      loads return zeros (no access), and they only feed outputs that
   //      are not stored. ---------------------------------------------------
   static_assert((NT / CPR) % 32 == 0, "row step of the DMA loads keeps the swizzle");
-  const int rows_x = min(GBM, M - m0), rows_w = min(GBN, N - n0);
+  const int rows_x = min(BM, M - m0), rows_w = min(BN, N - n0);
   const auto xr = make_rsrc(x + (long)m0 * K, rows_x * K * 2);
   const auto wr = make_rsrc(w + (long)n0 * K, rows_w * K * 2);
   uint32_t src0;
@@ -134,10 +141,11 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
   auto load = [&](int kt, int buf) {
     const int soff = __builtin_amdgcn_readfirstlane(kt * BK * 2);
 #pragma unroll
-    for (int j = 0; j < LPT; ++j) {
+    for (int j = 0; j < LPX; ++j)
       dma16(xr, smx[buf] + j * NT * 16 + wave * 1024, src0, soff + j * jstride);
+#pragma unroll
+    for (int j = 0; j < LPW; ++j)
       dma16(wr, smw[buf] + j * NT * 16 + wave * 1024, src0, soff + j * jstride);
-    }
   };
 
   // ---- fragment read offsets: lane reads row (block + l32), chunk 2 kk + g;
@@ -193,8 +201,8 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
         // unconditional (a branch here made the compiler wait for the
         // reads below before the products): past the last tile the refill
         // re-reads tile nk - 1 and the reads fetch unused fragments
-        __builtin_amdgcn_s_waitcnt(kVmWaitLgkm0<(NS - 2) * 2 * LPT>());  // tile t+1; our reads of t
-        __syncthreads();  // everyone's tile t+1 has landed; buffer cur is free
+        __builtin_amdgcn_s_waitcnt(kVmWaitLgkm0<(NS - 2) * (LPX + LPW)>());  // tile t+1; our reads of t
+        barrier_only();  // everyone's tile t+1 has landed; buffer cur is free
         load(min(t + NS, nk - 1), cur);
       }
       const int rs = kk + RA;  // each step: the reads RA steps ahead first, then products
@@ -209,8 +217,8 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
 
 #pragma unroll
   for (int s = 0; s < NS; ++s) load(min(s, nk - 1), s);
-  __builtin_amdgcn_s_waitcnt(kVmWaitLgkm0<(NS - 1) * 2 * LPT>());  // tile 0
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(kVmWaitLgkm0<(NS - 1) * (LPX + LPW)>());  // tile 0
+  barrier_only();
 #pragma unroll
   for (int s = 0; s < RA; ++s) rd(smx[0], smw[0], s, s);
   // buffers repeat every NS tiles, register sets every NSET / gcd(STEPS,
@@ -252,5 +260,5 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
 
 extern "C" __global__ __launch_bounds__(512) void teeny_gemm_bf16_nt(
     const bf16* x, const bf16* w, bf16* y, int M, int N, int K, int tiles_m, int tiles_n) {
-  gemm_bf16_nt<64, 2, 8, 2, 4, 2>(x, w, y, M, N, K, tiles_m, tiles_n);
+  gemm_bf16_nt<256, 256, 64, 2, 8, 2, 4, 2>(x, w, y, M, N, K, tiles_m, tiles_n);
 }
