@@ -36,34 +36,6 @@
 #include <numeric>
 #include <type_traits>
 
-// s_waitcnt immediate for vmcnt(n) alone (expcnt, lgkmcnt fields at their
-// maximum: not waited for); n < 64
-template <int n>
-constexpr int kVmWait() {
-  static_assert(n < 64, "vmcnt has 6 bits");
-  return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
-}
-// ... and lgkmcnt(0)
-template <int n>
-constexpr int kVmWaitLgkm0() {
-  return kVmWait<n>() & ~(15 << 8);
-}
-
-// s_barrier alone: __syncthreads() also waits for every memory operation in
-// flight (vmcnt(0)), which would wait for the tiles loading further ahead;
-// the caller waits for exactly what the barrier publishes.  The memory
-// clobber keeps the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
-
-// f(integral_constant<T>) for T = B .. E-1
-template <int B, int E, typename F>
-__device__ __forceinline__ void unroll_tiles(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    unroll_tiles<B + 1, E>(f);
-  }
-}
-
 namespace {
 
 
