@@ -339,6 +339,23 @@ int teeny_qkv_rope_split_partials_dev(const float* parts, int n_parts, void* q_o
                                       int n_heads_kv, int head_dim, float ln_rope_base,
                                       int dtype, hipStream_t stream);
 
+/* teeny_decode_qkv_attention_dev: a one-token decode step's attention in
+ * one launch, for position p = *n_past (read when the kernel runs): the
+ * QKV projection's K-split slabs parts[n_parts][batch][(Hq + 2 Hkv) D] are
+ * summed and rounded as by teeny_qkv_rope_split_partials_dev, k and v (k
+ * with RoPE) are written to cache row p when p < cache_len, and q (RoPE)
+ * attends to cache rows 0 .. min(p + 1, cache_len) - 1 as by
+ * teeny_decode_attention_dev; o [batch, Hq, D].  bf16, D 64 or 128,
+ * Hq / Hkv <= 32; no workspace.  One workgroup per (b, kv head) reads that
+ * head's rows, so it suits caches of a few thousand rows; longer ones
+ * spread better over the split-K teeny_decode_attention_dev.  No reference
+ * counterpart (the reference has no KV cache). */
+int teeny_decode_qkv_attention_dev(const float* parts, int n_parts, void* k_cache,
+                                   void* v_cache, void* o, int batch, int n_heads_q,
+                                   int n_heads_kv, int head_dim, int cache_len,
+                                   const int32_t* n_past, float ln_rope_base,
+                                   float softmax_scale, int dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,8 @@ _SIGNATURES = {
     "teeny_qkv_rope_split_dev": ([_p] * 4 + [_i, _i, _p] + [_i] * 4 + [_f, _i, _p], _i),
     "teeny_decode_attention_dev": ([_p] * 4 + [_i] * 3 + [_p] + [_i] * 3
                                    + [_f, _i, _p, _sz, _p], _i),
+    "teeny_decode_qkv_attention_dev": ([_p, _i, _p, _p, _p] + [_i] * 5 + [_p, _f, _f, _i, _p],
+                                       _i),
     "teeny_argmax_rows": ([_p, _p, _i, _i, _i, _p], _i),
     "teeny_linear_bf16": ([_p, _p, _p, _i, _i, _i, _p], _i),
     "teeny_linear_swiglu_bf16": ([_p, _p, _p, _i, _i, _i, _p], _i),

@@ -813,6 +813,33 @@ int teeny_qkv_rope_split_partials_dev(const float* parts, int n_parts, void* q_o
                 dim3(256), shmem, stream, args);
 }
 
+int teeny_decode_qkv_attention_dev(const float* parts, int n_parts, void* k_cache,
+                                   void* v_cache, void* o, int batch, int n_heads_q,
+                                   int n_heads_kv, int head_dim, int cache_len,
+                                   const int32_t* n_past, float ln_rope_base,
+                                   float softmax_scale, int dtype, hipStream_t stream) {
+  if (!parts || !k_cache || !v_cache || !o || !n_past) return TEENY_ERR_NULL_POINTER;
+  if (dtype != TEENY_BF16 || (head_dim != 64 && head_dim != 128)) return TEENY_ERR_UNSUPPORTED;
+  if (n_parts <= 0 || batch <= 0 || n_heads_q <= 0 || n_heads_kv <= 0 || cache_len <= 0 ||
+      n_heads_q % n_heads_kv != 0)
+    return TEENY_ERR_INVALID_SHAPE;
+  // the group's q rows are the 32 rows of one matrix product
+  if (n_heads_q / n_heads_kv > 32) return TEENY_ERR_UNSUPPORTED;
+  const int htot = n_heads_q + 2 * n_heads_kv;
+  long part_stride = (long)batch * htot * head_dim;
+  if (part_stride * n_parts >= kMaxElems ||
+      (long)batch * n_heads_kv * cache_len * head_dim >= kMaxElems)
+    return TEENY_ERR_INVALID_SHAPE;
+  if (!std::isfinite(ln_rope_base) || !scale_ok(softmax_scale, dtype))
+    return TEENY_ERR_INVALID_VALUE;
+  char name[48];
+  snprintf(name, sizeof name, "teeny_decode_qkv_attn_bf16_d%d", head_dim);
+  void* args[] = {&parts,      &n_parts,   &part_stride, &k_cache,      &v_cache,
+                  &o,          &n_heads_q, &n_heads_kv,  &n_past,       &cache_len,
+                  &ln_rope_base, &softmax_scale};
+  return launch(name, dim3((unsigned)(batch * n_heads_kv)), dim3(256), 0, stream, args);
+}
+
 static int decode_chunks(int n_keys) { return (n_keys + 255) / 256; }  // fp32 kernel
 
 // bf16 matrix-core kernel: keys per wavefront chosen so that one step runs

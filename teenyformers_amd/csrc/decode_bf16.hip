@@ -180,6 +180,229 @@ __device__ void decode_mfma(const bf16* __restrict__ q, const bf16* __restrict__
   }
 }
 
+// The whole attention of a graph-captured decode step in one launch, one
+// workgroup of 4 wavefronts per (b, kv head):
+//   1. the group's q heads and the kv head's k, v rows are summed from the
+//      QKV projection's K-split slabs (in slab order, rounded to bf16 as the
+//      unsplit product is stored), RoPE is applied at position n_past to q
+//      and k (qkv_rope_split's arithmetic), k and v are written to the cache
+//      row n_past and q is kept in LDS;
+//   2. the cache rows 0 .. min(n_past + 1, cache_len) - 1 are split between
+//      the 4 wavefronts, each running decode_mfma's loop on its own LDS
+//      buffers;
+//   3. the 4 partials (max, sum, unnormalised O) are merged in LDS and
+//      o [B, Hq, D] is stored.
+// It replaces the QKV split, the split-K decode kernel and the combine
+// kernel of the unfused path with one launch and no partials in HBM.
+constexpr int kDqWaves = 4;
+
+template <int D>
+struct __attribute__((aligned(16))) DecQkvSmem {
+  union {
+    struct {
+      char k[kDqWaves][2][TK * D * 2];
+      char v[kDqWaves][2][TK * D * 2];
+    } t;
+    struct {
+      float m[kDqWaves][32];
+      float l[kDqWaves][32];
+      float o[kDqWaves][32 * D];
+    } c;
+  } u;
+  bf16 q[32 * D];  // the group's RoPE'd q rows
+};
+
+template <int D>
+__device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, long part_stride,
+                                bf16* __restrict__ kc, bf16* __restrict__ vc,
+                                bf16* __restrict__ o, int hq, int hkv,
+                                const int* __restrict__ n_past, int cache_len, float ln_base,
+                                float scale) {
+  constexpr int DC = D / 16, DT = D / 32, CPR = D / 8;
+  constexpr int TILE = TK * D * 2;  // bytes of a K or V tile
+  constexpr int NLD = TILE / 1024;  // 16-byte-per-lane loads per tile
+  constexpr int VN = 8;             // bf16 per 16-byte vector
+  __shared__ DecQkvSmem<D> sm;
+
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kvh = blockIdx.x, b = kvh / hkv, hk = kvh - b * hkv;
+  const int group = hq / hkv;
+  const int htot = hq + 2 * hkv;
+  const int pos = __builtin_amdgcn_readfirstlane(*n_past);
+  const int n_keys = __builtin_amdgcn_readfirstlane(min(pos + 1, cache_len));
+
+  // ---- 1. q, k, v of position pos -------------------------------------------
+  const float c = (-2.0f * ln_base) / (float)D;
+  for (int i = tid; i < (group + 2) * (D / VN); i += kDqWaves * 64) {
+    const int hh = i / (D / VN), vv = i - hh * (D / VN);
+    const int row = hh < group ? hk * group + hh : (hh == group ? hq + hk : hq + hkv + hk);
+    float in[VN];
+    ld_parts<bf16, VN>(parts + ((long)b * htot + row) * D + vv * VN, part_stride, n_parts, in);
+    float out[VN];
+    if (hh <= group) {  // q and k: RoPE on the interleaved pairs
+#pragma unroll
+      for (int j = 0; j < VN / 2; ++j) {
+        const int kk = vv * (VN / 2) + j;
+        const float inv = (float)exp((double)((float)kk * c));
+        const float theta = (float)pos * inv;
+        float sn, cn;
+        sincosf(theta, &sn, &cn);
+        out[2 * j] = in[2 * j] * cn - in[2 * j + 1] * sn;
+        out[2 * j + 1] = in[2 * j] * sn + in[2 * j + 1] * cn;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < VN; ++j) out[j] = in[j];
+    }
+    if (hh < group) {
+      Vec16<bf16>::store(sm.q + hh * D + vv * VN, out);
+    } else if (pos >= 0 && pos < cache_len) {
+      bf16* cache = hh == group ? kc : vc;
+      Vec16<bf16>::store(cache + ((long)kvh * cache_len + pos) * D + vv * VN, out);
+    }
+  }
+  // the new cache row has reached memory (the barrier waits for every
+  // store), so this workgroup's tile loads below read it
+  __syncthreads();
+
+  bf16x8 qreg[DC];
+#pragma unroll
+  for (int cc = 0; cc < DC; ++cc)
+    qreg[cc] = l32 < group ? as_bf16x8(*reinterpret_cast<const u32x4*>(
+                                 sm.q + l32 * D + 16 * cc + 8 * g))
+                           : as_bf16x8(u32x4{0, 0, 0, 0});
+
+  // ---- 2. this wavefront's share of the keys (decode_mfma's loop) -----------
+  const int kpw = ((n_keys + kDqWaves - 1) / kDqWaves + TK - 1) / TK * TK;
+  const int k0 = wave * kpw;
+  const int k1 = min(k0 + kpw, n_keys);
+  const auto krs = make_rsrc(kc + (long)kvh * cache_len * D, cache_len * D * 2);
+  const auto vrs = make_rsrc(vc + (long)kvh * cache_len * D, cache_len * D * 2);
+  uint32_t ksrc[NLD], vsrc[NLD];
+#pragma unroll
+  for (int i = 0; i < NLD; ++i) {
+    ksrc[i] = swz<SWZ_ROW, D>(i * 64 + lane) * 16;
+    vsrc[i] = swz<SWZ_DUAL, D>(i * 64 + lane) * 16;
+  }
+  auto load = [&](int t0, int buf) {
+    const int soff = __builtin_amdgcn_readfirstlane(t0 * D * 2);
+    char* kd = sm.u.t.k[wave][buf];
+    char* vd = sm.u.t.v[wave][buf];
+    if (t0 + TK <= n_keys) {
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) {
+        dma16(krs, kd + i * 1024, ksrc[i], soff);
+        dma16(vrs, vd + i * 1024, vsrc[i], soff);
+      }
+    } else {  // rows at or past n_keys re-read row n_keys - 1 (masked)
+      const int lastrow = n_keys - 1 - t0;
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) {
+        dma16(krs, kd + i * 1024,
+              min((int)ksrc[i] / (2 * D), lastrow) * (2 * D) + ksrc[i] % (2 * D), soff);
+        dma16(vrs, vd + i * 1024,
+              min((int)vsrc[i] / (2 * D), lastrow) * (2 * D) + vsrc[i] % (2 * D), soff);
+      }
+    }
+  };
+  int k_off[DC];
+#pragma unroll
+  for (int cc = 0; cc < DC; ++cc) k_off[cc] = swz<SWZ_ROW, D>(l32 * CPR + 2 * cc + g) * 16;
+  int v_off[DT][2];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int r = 8 * e + 4 * g + ((lane & 15) >> 2);
+      const int col = 32 * t + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+      v_off[t][e] = swz<SWZ_DUAL, D>(r * CPR + col / 8) * 16 + (col % 8) * 2;
+    }
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
+  float m = -INFINITY, l = 0.0f;  // log2-domain max of scale * score; this lane's sum
+  const float sl2 = scale * kLog2e;
+  const int n_tiles = k0 < k1 ? (k1 - k0 + TK - 1) / TK : 0;
+  if (n_tiles > 0) load(k0, 0);
+  for (int it = 0; it < n_tiles; ++it) {
+    const int buf = it & 1, t0 = k0 + it * TK;
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);  // tile it has landed
+    if (it + 1 < n_tiles) load(t0 + TK, buf ^ 1);
+    const char* kt = sm.u.t.k[wave][buf];
+    const char* vt = sm.u.t.v[wave][buf];
+    u32x4 kr[DC];
+#pragma unroll
+    for (int cc = 0; cc < DC; ++cc) kr[cc] = *reinterpret_cast<const u32x4*>(kt + k_off[cc]);
+    f32x16 s = f32x16{};
+#pragma unroll
+    for (int cc = 0; cc < DC; ++cc) s = mfma32(as_bf16x8(kr[cc]), qreg[cc], s);
+    sched_group(kDsRead, DC);
+    sched_group(kMfma, DC);
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (t0 + 8 * (r >> 2) + 4 * g + (r & 3) >= k1) s[r] = -INFINITY;
+    float mx = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+    mx = fmaxf(mx, other_half(mx));
+    const float m_new = fmaxf(m, mx * sl2);  // finite: tile it has a key below k1
+    const float alpha = fast_exp2(m - m_new);
+    m = m_new;
+    l *= alpha;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] *= alpha;
+    uint32_t pb[8];
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      pb[r >> 1] = pack_bf16x2(fast_exp2(__builtin_fmaf(s[r], sl2, -m)),
+                               fast_exp2(__builtin_fmaf(s[r + 1], sl2, -m)));
+      l = add_bf16x2(pb[r >> 1], l);
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const bf16x8 bop = as_bf16x8(u32x4{pb[4 * hh], pb[4 * hh + 1], pb[4 * hh + 2], pb[4 * hh + 3]});
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const char* pp = vt + hh * 16 * D * 2;
+        u32x2 a0 = lds_read_tr(pp + v_off[t][0]), a1 = lds_read_tr(pp + v_off[t][1]);
+        acc[t] = mfma32(as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]}), bop, acc[t]);
+      }
+    }
+  }
+  const float l_tot = l + other_half(l);
+
+  // ---- 3. merge the wavefronts' partials ------------------------------------
+  __syncthreads();  // every wavefront is done with its tiles
+  if (l32 < group) {
+    if (g == 0) {
+      sm.u.c.m[wave][l32] = m;  // -inf for a wavefront without keys
+      sm.u.c.l[wave][l32] = l_tot;
+    }
+    float* orow = sm.u.c.o[wave] + l32 * D;
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) orow[32 * t + 8 * (r >> 2) + 4 * g + (r & 3)] = acc[t][r];
+  }
+  __syncthreads();
+  for (int i = tid; i < group * D; i += kDqWaves * 64) {
+    const int hh = i / D, d = i - hh * D;
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDqWaves; ++w) mm = fmaxf(mm, sm.u.c.m[w][hh]);
+    float num = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kDqWaves; ++w) {
+      const float e = fast_exp2(sm.u.c.m[w][hh] - mm);  // 0 for a wavefront without keys
+      num += e * sm.u.c.o[w][hh * D + d];
+      den += e * sm.u.c.l[w][hh];
+    }
+    o[((long)b * hq + hk * group + hh) * D + d] = (bf16)(num / den);
+  }
+}
+
 }  // namespace
 
 #define TEENY_DECODE_BF16_INST(D)                                                                \
@@ -193,3 +416,14 @@ __device__ void decode_mfma(const bf16* __restrict__ q, const bf16* __restrict__
 
 TEENY_DECODE_BF16_INST(64)
 TEENY_DECODE_BF16_INST(128)
+
+#define TEENY_DECODE_QKV_INST(D)                                                                 \
+  extern "C" __global__ __launch_bounds__(256) void teeny_decode_qkv_attn_bf16_d##D(            \
+      const float* parts, int n_parts, long part_stride, bf16* kc, bf16* vc, bf16* o, int hq,    \
+      int hkv, const int* n_past, int cache_len, float ln_base, float scale) {                   \
+    decode_qkv_attn<D>(parts, n_parts, part_stride, kc, vc, o, hq, hkv, n_past, cache_len,      \
+                       ln_base, scale);                                                          \
+  }
+
+TEENY_DECODE_QKV_INST(64)
+TEENY_DECODE_QKV_INST(128)

@@ -186,9 +186,14 @@ class Llama:
         p = f"model.layers.{i}.self_attn."
         # [B, S, (Hq+2Hkv) D]; K-split fp32 slabs at decode sizes
         qkv = ops.linear_split(n1, w[p + "qkv_proj.weight"])
+        scale = cfg.softmax_scale()
+        if isinstance(pos0, torch.Tensor) and self._fused_decode(qkv, cache):
+            # one launch: QKV split, RoPE, cache write and attention
+            o = ops.decode_qkv_attention(qkv, cache.k[i], cache.v[i], pos0, Hq, Hkv,
+                                         cfg.rope_base, scale)
+            return ops.linear_split(o.view(B, 1, Hq * D), w[p + "o_proj.weight"])
         q = torch.empty((B, Hq, S, D), dtype=n1.dtype, device=n1.device)
         ops.qkv_rope_split(qkv, q, cache.k[i], cache.v[i], pos0, Hq, Hkv, cfg.rope_base)
-        scale = cfg.softmax_scale()
         if isinstance(pos0, torch.Tensor):  # graph decode: the position is on the device
             if S != 1:
                 raise ValueError("a device position is for one-token decode steps")
@@ -207,6 +212,15 @@ class Llama:
         # one position: [B, Hq, 1, D] is already the merged [B, 1, Hq D] layout
         att = o.view(B, S, Hq * D) if S == 1 else ops.merge_heads(o)
         return ops.linear_split(att, w[p + "o_proj.weight"])
+
+    def _fused_decode(self, qkv, cache: KVCache) -> bool:
+        """Whether a one-token step runs teeny_decode_qkv_attention_dev: bf16
+        K-split QKV slabs, D 64 or 128, up to 32 q heads per kv head, and a
+        cache short enough for one workgroup per (b, kv head)."""
+        cfg = self.cfg
+        return (isinstance(qkv, ops.Partials) and qkv.dtype == torch.bfloat16
+                and cfg.head_dim() in (64, 128) and cfg.n_heads // cfg.n_kv_heads() <= 32
+                and cache.capacity <= 4096)
 
     def _decode_ws(self, B: int, cache: KVCache, device) -> torch.Tensor:
         """Split-K workspace for decode attention over the whole cache."""
@@ -234,6 +248,11 @@ class Llama:
         cfg, w = self.cfg, self.w
         x = ops.token_embed(ids.to(torch.int32).contiguous(), w["model.embed_tokens.weight"])
         eps = cfg.eps
+        pos = pos0
+        if ids.shape[1] == 1 and not isinstance(pos0, torch.Tensor) and pos0 > 0:
+            # a one-token step takes its position from device memory, as the
+            # captured graph does, so both run the same kernels
+            pos = torch.tensor([pos0], dtype=torch.int32, device=ids.device)
         delta = None
         for i in range(cfg.n_layers):
             p = f"model.layers.{i}."
@@ -242,7 +261,7 @@ class Llama:
             else:  # x = x + ffn(...) fused into this block's input norm
                 n1, x, _ = ops.fused_add_rmsnorm(delta, x, w[p + "input_layernorm.weight"], eps)
             x_in = x
-            a = self._attention(i, n1, cache, pos0)
+            a = self._attention(i, n1, cache, pos)
             n2, x, _ = ops.fused_add_rmsnorm(a, x, w[p + "post_attention_layernorm.weight"], eps)
             delta = self._ffn(i, n2)
             if trace is not None:

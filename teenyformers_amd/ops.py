@@ -431,6 +431,31 @@ def decode_attention(q, k_cache, v_cache, n_keys: int, softmax_scale: float | No
     return out
 
 
+def decode_qkv_attention(qkv: "Partials", k_cache, v_cache, n_past, n_heads_q: int,
+                         n_heads_kv: int, rope_base: float, softmax_scale: float | None = None,
+                         out=None):
+    """A one-token step's attention in one launch: qkv (the QKV projection's
+    K-split Partials, [B, 1, (Hq+2Hkv) D]) is split with RoPE at position
+    *n_past (a one-element int32 device tensor), k / v are written to cache
+    row *n_past, and q attends to rows 0 .. *n_past.  Returns o [B, Hq, D]."""
+    if not isinstance(qkv, Partials):
+        raise TypeError("decode_qkv_attention takes the QKV projection's K-split slabs")
+    _dev(qkv.slabs, k_cache, v_cache)
+    if n_past.dtype != torch.int32 or not n_past.is_cuda:
+        raise TypeError("n_past must be an int32 CUDA tensor")
+    B, S, _ = qkv.shape
+    if S != 1:
+        raise ValueError("decode_qkv_attention is for one-token steps")
+    D, L = k_cache.shape[3], k_cache.shape[2]
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    out = torch.empty((B, n_heads_q, D), dtype=k_cache.dtype, device=k_cache.device) \
+        if out is None else out
+    call("teeny_decode_qkv_attention_dev", _p(qkv.slabs), qkv.n, _p(k_cache), _p(v_cache),
+         _p(out), B, n_heads_q, n_heads_kv, D, L, _p(n_past), _ln(rope_base), scale,
+         _code(k_cache), _stream())
+    return out
+
+
 def argmax_rows(x, out=None):
     """x [rows, cols] -> int64 [rows]: the last index of each row's maximum,
     the reference's greedy choice (examples/llama_generate.rs:252-257,

@@ -173,3 +173,22 @@ def test_decode_ops_validation(L):
                                                9.21, BF16, None) == SHAPE  # 8 % 3
     assert L.teeny_argmax_rows(None, P, 4, 10, BF16, None) == NULLP
     assert L.teeny_argmax_rows(P, P, 0, 10, BF16, None) == SHAPE
+
+
+def test_decode_qkv_attention_validation(L):
+    def call(**kw):
+        a = dict(parts=P, n=4, k=P, v=P, o=P, b=2, hq=32, hkv=8, d=128, cl=640, pos=P,
+                 lnb=13.1, scale=0.088, dtype=BF16)
+        a.update(kw)
+        return L.teeny_decode_qkv_attention_dev(a["parts"], a["n"], a["k"], a["v"], a["o"], a["b"],
+                                                a["hq"], a["hkv"], a["d"], a["cl"], a["pos"],
+                                                a["lnb"], a["scale"], a["dtype"], None)
+    assert call(parts=None) == NULLP
+    assert call(pos=None) == NULLP
+    assert call(dtype=F32) == UNSUP
+    assert call(d=96) == UNSUP
+    assert call(hq=64, hkv=1) == UNSUP  # 64 q heads per kv head: more than one product's rows
+    assert call(hq=6, hkv=4) == SHAPE
+    assert call(n=0) == SHAPE
+    assert call(scale=-1.0) == VALUE
+    assert call(lnb=float("nan")) == VALUE

@@ -242,6 +242,48 @@ def test_device_position_variants(cuda, dtype):
     assert torch.equal(kd, kc0) and torch.equal(vd, vc0)
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,D,L", [
+    (4, 32, 8, 128, 640),   # the Llama-3-8B decode shape
+    (3, 8, 1, 64, 300),     # 8 q heads on one kv head, cache off the 32-key tile
+    (2, 32, 1, 128, 1000),  # a 32-head group: every row of the score product
+])
+def test_decode_qkv_attention_fused(cuda, B, Hq, Hkv, D, L):
+    """The one-launch decode step (QKV split + RoPE + cache write +
+    attention) writes the same cache rows as teeny_qkv_rope_split_partials_dev
+    (bit for bit) and its output matches the oracle's attention of that q
+    over the cache rows 0 .. pos; rows past pos hold NaN and are not read; a
+    position past the cache writes nothing."""
+    rng = np.random.default_rng(B * 131 + Hq + D + L)
+    d = 512
+    n = (Hq + 2 * Hkv) * D
+    x = _bf16_dev(rng.standard_normal((B, 1, d)).astype(np.float32))
+    wq = _bf16_dev((0.05 * rng.standard_normal((n, d))).astype(np.float32))
+    pq = ops.linear_split(x, wq, 128)
+    assert pq.n == 4
+    kc0 = _bf16_dev(rng.standard_normal((B, Hkv, L, D)).astype(np.float32))
+    vc0 = _bf16_dev(rng.standard_normal((B, Hkv, L, D)).astype(np.float32))
+    scale = 1.0 / math.sqrt(D)
+    for pos in (0, 37 % L, L - 1, L):
+        kc, vc = kc0.clone(), vc0.clone()
+        kc[:, :, pos + 1:] = float("nan")
+        vc[:, :, pos + 1:] = float("nan")
+        pdev = torch.tensor([pos], dtype=torch.int32, device="cuda")
+        q = torch.empty((B, Hq, 1, D), dtype=torch.bfloat16, device="cuda")
+        k1, v1, k2, v2 = kc.clone(), vc.clone(), kc.clone(), vc.clone()
+        ops.qkv_rope_split(pq, q, k1, v1, pdev, Hq, Hkv, 5e5)
+        o = ops.decode_qkv_attention(pq, k2, v2, pdev, Hq, Hkv, 5e5, scale)
+        torch.cuda.synchronize()
+        print(f"decode_qkv: B{B} Hq{Hq} Hkv{Hkv} D{D} L{L} pos {pos}", flush=True)
+        assert torch.equal(k1.view(torch.int16), k2.view(torch.int16))
+        assert torch.equal(v1.view(torch.int16), v2.view(torch.int16))
+        n_keys = min(pos + 1, L)
+        want, _ = O.fa2_fwd(host(q), host(k1[:, :, :n_keys]), host(v1[:, :, :n_keys]), scale,
+                            causal=False)
+        got = host(o)
+        assert np.isfinite(got).all()
+        assert rel_l2(got, want[:, :, 0]) <= 5e-3 and np.abs(got - want[:, :, 0]).max() <= 2e-2
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_generate_graph_equals_eager(cuda, dtype):
     """Greedy ids from the decode step captured in a HIP graph and replayed
