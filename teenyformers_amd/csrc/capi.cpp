@@ -837,7 +837,7 @@ int teeny_decode_qkv_attention_dev(const float* parts, int n_parts, void* k_cach
   void* args[] = {&parts,      &n_parts,   &part_stride, &k_cache,      &v_cache,
                   &o,          &n_heads_q, &n_heads_kv,  &n_past,       &cache_len,
                   &ln_rope_base, &softmax_scale};
-  return launch(name, dim3((unsigned)(batch * n_heads_kv)), dim3(256), 0, stream, args);
+  return launch(name, dim3((unsigned)(batch * n_heads_kv)), dim3(512), 0, stream, args);
 }
 
 static int decode_chunks(int n_keys) { return (n_keys + 255) / 256; }  // fp32 kernel

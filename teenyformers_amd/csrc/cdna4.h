@@ -15,13 +15,13 @@ DEVI f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// max of three floats in one instruction.  fmaxf on MFMA results costs an
-// extra canonicalising v_max per operand; scores are never signalling NaNs.
-DEVI float max3(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
+// max of three floats (one v_max3_f32).  A builtin, not inline asm: the
+// compiler must see the instruction to keep the wait states that an MFMA
+// result read right after the product, or an MFMA operand register
+// overwritten right after its issue, requires.  Files that take their
+// inputs from MFMA results are compiled with -fno-honor-nans, so no
+// canonicalising v_max is added per operand (scores are never NaN).
+DEVI float max3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 // the value held by lane l ^ 32 (v_permlane32_swap)
 DEVI float other_half(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
@@ -38,7 +38,7 @@ DEVI float add_bf16x2(uint32_t w, float acc) {
 
 // Instruction classes of __builtin_amdgcn_sched_group_barrier: the machine
 // scheduler fills the groups in the order they are declared.
-constexpr int kMfma = 0x008, kDsRead = 0x100;
+constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
 #define sched_group(mask, n) __builtin_amdgcn_sched_group_barrier((mask), (n), 0)
 // Keeps the computation of x above this point: values used only in the next
 // loop iteration would otherwise be sunk below the barrier that ends one,

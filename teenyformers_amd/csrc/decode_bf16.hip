@@ -23,8 +23,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
 // s_waitcnt immediate for vmcnt(0) alone (expcnt and lgkmcnt fields at their
-// maximum: not waited for)
+// maximum: not waited for), and for lgkmcnt(0) alone
 constexpr int kVmcnt0 = (7 << 4) | (15 << 8);
+constexpr int kLgkmcnt0 = 15 | (3 << 14) | (7 << 4);
 
 template <int D>
 struct __attribute__((aligned(16))) DecSmem {
@@ -181,27 +182,29 @@ __device__ void decode_mfma(const bf16* __restrict__ q, const bf16* __restrict__
 }
 
 // The whole attention of a graph-captured decode step in one launch, one
-// workgroup of 4 wavefronts per (b, kv head):
+// workgroup of 8 wavefronts per (b, kv head):
 //   1. the group's q heads and the kv head's k, v rows are summed from the
 //      QKV projection's K-split slabs (in slab order, rounded to bf16 as the
 //      unsplit product is stored), RoPE is applied at position n_past to q
 //      and k (qkv_rope_split's arithmetic), k and v are written to the cache
 //      row n_past and q is kept in LDS;
 //   2. the cache rows 0 .. min(n_past + 1, cache_len) - 1 are split between
-//      the 4 wavefronts, each running decode_mfma's loop on its own LDS
-//      buffers;
-//   3. the 4 partials (max, sum, unnormalised O) are merged in LDS and
+//      the 8 wavefronts, each running decode_mfma's loop on its own LDS
+//      buffer of one 32-key tile (a wavefront's first tile, unless it holds
+//      row n_past, is requested before step 1, so the two latencies
+//      overlap);
+//   3. the 8 partials (max, sum, unnormalised O) are merged in LDS and
 //      o [B, Hq, D] is stored.
 // It replaces the QKV split, the split-K decode kernel and the combine
 // kernel of the unfused path with one launch and no partials in HBM.
-constexpr int kDqWaves = 4;
+constexpr int kDqWaves = 8;
 
 template <int D>
 struct __attribute__((aligned(16))) DecQkvSmem {
   union {
     struct {
-      char k[kDqWaves][2][TK * D * 2];
-      char v[kDqWaves][2][TK * D * 2];
+      char k[kDqWaves][TK * D * 2];
+      char v[kDqWaves][TK * D * 2];
     } t;
     struct {
       float m[kDqWaves][32];
@@ -231,6 +234,45 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
   const int htot = hq + 2 * hkv;
   const int pos = __builtin_amdgcn_readfirstlane(*n_past);
   const int n_keys = __builtin_amdgcn_readfirstlane(min(pos + 1, cache_len));
+
+  // this wavefront's keys k0 .. k1 - 1, in 32-key tiles through its LDS buffer
+  const int kpw = ((n_keys + kDqWaves - 1) / kDqWaves + TK - 1) / TK * TK;
+  const int k0 = wave * kpw;
+  const int k1 = min(k0 + kpw, n_keys);
+  const int n_tiles = k0 < k1 ? (k1 - k0 + TK - 1) / TK : 0;
+  const auto krs = make_rsrc(kc + (long)kvh * cache_len * D, cache_len * D * 2);
+  const auto vrs = make_rsrc(vc + (long)kvh * cache_len * D, cache_len * D * 2);
+  uint32_t ksrc[NLD], vsrc[NLD];
+#pragma unroll
+  for (int i = 0; i < NLD; ++i) {
+    ksrc[i] = swz<SWZ_ROW, D>(i * 64 + lane) * 16;
+    vsrc[i] = swz<SWZ_DUAL, D>(i * 64 + lane) * 16;
+  }
+  // keys t0 .. t0+TK-1; rows at or past n_keys re-read row n_keys - 1 (masked)
+  auto load = [&](int t0) {
+    const int soff = __builtin_amdgcn_readfirstlane(t0 * D * 2);
+    char* kd = sm.u.t.k[wave];
+    char* vd = sm.u.t.v[wave];
+    if (t0 + TK <= n_keys) {
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) {
+        dma16(krs, kd + i * 1024, ksrc[i], soff);
+        dma16(vrs, vd + i * 1024, vsrc[i], soff);
+      }
+    } else {
+      const int lastrow = n_keys - 1 - t0;
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) {
+        dma16(krs, kd + i * 1024,
+              min((int)ksrc[i] / (2 * D), lastrow) * (2 * D) + ksrc[i] % (2 * D), soff);
+        dma16(vrs, vd + i * 1024,
+              min((int)vsrc[i] / (2 * D), lastrow) * (2 * D) + vsrc[i] % (2 * D), soff);
+      }
+    }
+  };
+  // the first tile goes out now unless it holds row pos (written below)
+  const bool early = n_tiles > 0 && k0 + TK <= pos;
+  if (early) load(k0);
 
   // ---- 1. q, k, v of position pos -------------------------------------------
   const float c = (-2.0f * ln_base) / (float)D;
@@ -265,6 +307,7 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
   // the new cache row has reached memory (the barrier waits for every
   // store), so this workgroup's tile loads below read it
   __syncthreads();
+  if (n_tiles > 0 && !early) load(k0);
 
   bf16x8 qreg[DC];
 #pragma unroll
@@ -273,39 +316,7 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
                                  sm.q + l32 * D + 16 * cc + 8 * g))
                            : as_bf16x8(u32x4{0, 0, 0, 0});
 
-  // ---- 2. this wavefront's share of the keys (decode_mfma's loop) -----------
-  const int kpw = ((n_keys + kDqWaves - 1) / kDqWaves + TK - 1) / TK * TK;
-  const int k0 = wave * kpw;
-  const int k1 = min(k0 + kpw, n_keys);
-  const auto krs = make_rsrc(kc + (long)kvh * cache_len * D, cache_len * D * 2);
-  const auto vrs = make_rsrc(vc + (long)kvh * cache_len * D, cache_len * D * 2);
-  uint32_t ksrc[NLD], vsrc[NLD];
-#pragma unroll
-  for (int i = 0; i < NLD; ++i) {
-    ksrc[i] = swz<SWZ_ROW, D>(i * 64 + lane) * 16;
-    vsrc[i] = swz<SWZ_DUAL, D>(i * 64 + lane) * 16;
-  }
-  auto load = [&](int t0, int buf) {
-    const int soff = __builtin_amdgcn_readfirstlane(t0 * D * 2);
-    char* kd = sm.u.t.k[wave][buf];
-    char* vd = sm.u.t.v[wave][buf];
-    if (t0 + TK <= n_keys) {
-#pragma unroll
-      for (int i = 0; i < NLD; ++i) {
-        dma16(krs, kd + i * 1024, ksrc[i], soff);
-        dma16(vrs, vd + i * 1024, vsrc[i], soff);
-      }
-    } else {  // rows at or past n_keys re-read row n_keys - 1 (masked)
-      const int lastrow = n_keys - 1 - t0;
-#pragma unroll
-      for (int i = 0; i < NLD; ++i) {
-        dma16(krs, kd + i * 1024,
-              min((int)ksrc[i] / (2 * D), lastrow) * (2 * D) + ksrc[i] % (2 * D), soff);
-        dma16(vrs, vd + i * 1024,
-              min((int)vsrc[i] / (2 * D), lastrow) * (2 * D) + vsrc[i] % (2 * D), soff);
-      }
-    }
-  };
+  // ---- 2. attention over this wavefront's keys (decode_mfma's loop) ---------
   int k_off[DC];
 #pragma unroll
   for (int cc = 0; cc < DC; ++cc) k_off[cc] = swz<SWZ_ROW, D>(l32 * CPR + 2 * cc + g) * 16;
@@ -324,14 +335,11 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
   for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
   float m = -INFINITY, l = 0.0f;  // log2-domain max of scale * score; this lane's sum
   const float sl2 = scale * kLog2e;
-  const int n_tiles = k0 < k1 ? (k1 - k0 + TK - 1) / TK : 0;
-  if (n_tiles > 0) load(k0, 0);
+  const char* kt = sm.u.t.k[wave];
+  const char* vt = sm.u.t.v[wave];
   for (int it = 0; it < n_tiles; ++it) {
-    const int buf = it & 1, t0 = k0 + it * TK;
+    const int t0 = k0 + it * TK;
     __builtin_amdgcn_s_waitcnt(kVmcnt0);  // tile it has landed
-    if (it + 1 < n_tiles) load(t0 + TK, buf ^ 1);
-    const char* kt = sm.u.t.k[wave][buf];
-    const char* vt = sm.u.t.v[wave][buf];
     u32x4 kr[DC];
 #pragma unroll
     for (int cc = 0; cc < DC; ++cc) kr[cc] = *reinterpret_cast<const u32x4*>(kt + k_off[cc]);
@@ -360,15 +368,24 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
                                fast_exp2(__builtin_fmaf(s[r + 1], sl2, -m)));
       l = add_bf16x2(pb[r >> 1], l);
     }
+    u32x4 va[2][DT];
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const bf16x8 bop = as_bf16x8(u32x4{pb[4 * hh], pb[4 * hh + 1], pb[4 * hh + 2], pb[4 * hh + 3]});
+    for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
         const char* pp = vt + hh * 16 * D * 2;
         u32x2 a0 = lds_read_tr(pp + v_off[t][0]), a1 = lds_read_tr(pp + v_off[t][1]);
-        acc[t] = mfma32(as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]}), bop, acc[t]);
+        va[hh][t] = u32x4{a0[0], a0[1], a1[0], a1[1]};
       }
+    // every read of the buffer has returned: the next tile may refill it
+    // while the products run
+    __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
+    if (it + 1 < n_tiles) load(t0 + TK);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const bf16x8 bop = as_bf16x8(u32x4{pb[4 * hh], pb[4 * hh + 1], pb[4 * hh + 2], pb[4 * hh + 3]});
+#pragma unroll
+      for (int t = 0; t < DT; ++t) acc[t] = mfma32(as_bf16x8(va[hh][t]), bop, acc[t]);
     }
   }
   const float l_tot = l + other_half(l);
@@ -418,7 +435,7 @@ TEENY_DECODE_BF16_INST(64)
 TEENY_DECODE_BF16_INST(128)
 
 #define TEENY_DECODE_QKV_INST(D)                                                                 \
-  extern "C" __global__ __launch_bounds__(256) void teeny_decode_qkv_attn_bf16_d##D(            \
+  extern "C" __global__ __launch_bounds__(512) void teeny_decode_qkv_attn_bf16_d##D(            \
       const float* parts, int n_parts, long part_stride, bf16* kc, bf16* vc, bf16* o, int hq,    \
       int hkv, const int* n_past, int cache_len, float ln_base, float scale) {                   \
     decode_qkv_attn<D>(parts, n_parts, part_stride, kc, vc, o, hq, hkv, n_past, cache_len,      \

@@ -51,8 +51,9 @@ DEVI int gpos(int r, int c) {
 // BM x BN: the workgroup's tile of y; BK: K per LDS tile; NS: tiles in
 // flight (LDS buffers); WAVES: wavefronts per workgroup, WGM of them along M
 // (WAVES / WGM along N); GROUP_M: tile-rows per group of the tile order; RA:
-// 16-k steps of fragment read-ahead.
-template <int BM, int BN, int BK, int NS, int WAVES, int WGM, int GROUP_M, int RA>
+// 16-k steps of fragment read-ahead; IL: the refill's loads are issued IL at a
+// time between the products of the step that issues them (0: all at once).
+template <int BM, int BN, int BK, int NS, int WAVES, int WGM, int GROUP_M, int RA, int IL = 0>
 __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const bf16* __restrict__ w,
                              bf16* __restrict__ y, int M, int N, int K, int tiles_m,
                              int tiles_n) {
@@ -182,7 +183,16 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
       else rd(smx[nxt], smw[nxt], rs - STEPS, (s0 + rs) % NSET);
       mm((s0 + kk) % NSET);
       sched_group(kDsRead, I + J);
-      sched_group(kMfma, I * J);
+      if (IL && kk == STEPS - RA) {
+        // the refill's loads between the products, IL at a time
+#pragma unroll
+        for (int q = 0; q < I * J; ++q) {
+          sched_group(kMfma, 1);
+          if (q * IL < LPX + LPW) sched_group(kVmemRead, IL);
+        }
+      } else {
+        sched_group(kMfma, I * J);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -206,6 +216,9 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
     });
   }
 
+  // the refills issued past the last tile land before the workgroup's LDS
+  // is released
+  __builtin_amdgcn_s_waitcnt(kVmWait<0>());
   // ---- y: lane = row m (l32 of each 32-row block), registers 4q..4q+3 are
   //      columns 8q + 4g .. +3 of the 32-column block ----------------------
 #pragma unroll
@@ -232,5 +245,5 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
 
 extern "C" __global__ __launch_bounds__(512) void teeny_gemm_bf16_nt(
     const bf16* x, const bf16* w, bf16* y, int M, int N, int K, int tiles_m, int tiles_n) {
-  gemm_bf16_nt<256, 256, 64, 2, 8, 2, 4, 2>(x, w, y, M, N, K, tiles_m, tiles_n);
+  gemm_bf16_nt<256, 256, 64, 2, 8, 2, 4, 2, 1>(x, w, y, M, N, K, tiles_m, tiles_n);
 }

@@ -245,14 +245,25 @@ def test_fa2_bf16_random_shapes(cuda, B, Hq, Hkv, Sq, Sk, D, causal):
     check_bf16("dV", host(dv), dve)
 
 
-def test_fa2_bf16_bwd_deterministic(cuda):
-    q, k, v, do = inputs(40, 1, 8, 2, 700, 700, 128, bf16=True)
+@pytest.mark.parametrize("B,Hq,Hkv,S,D", [(1, 8, 2, 700, 128), (3, 8, 2, 777, 128),
+                                         (16, 32, 8, 512, 128), (2, 8, 8, 1000, 64)])
+def test_fa2_bf16_deterministic(cuda, B, Hq, Hkv, S, D):
+    """Every output bit-identical across calls: O, LSE, dQ, dK, dV (and
+    the fp32-gradient option).  A row maximum that read a matrix product's
+    result too early once made whole rows of O and LSE differ by an ulp
+    from call to call at D = 128."""
+    q, k, v, do = inputs(40 + S, B, Hq, Hkv, S, S, D, bf16=True)
     qd, kd, vd, dod = (dev(t, torch.bfloat16) for t in (q, k, v, do))
-    o, lse = ops.flash_attn2_fwd(qd, kd, vd)
-    a = ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod)
-    b = ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod)
-    # dK/dV are register accumulations in a fixed order
-    assert torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])
+    runs = []
+    for _ in range(3):
+        o, lse = ops.flash_attn2_fwd(qd, kd, vd)
+        g = ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod)
+        g32 = ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod, grad_f32=True)
+        runs.append((o, lse) + tuple(g) + tuple(g32))
+    for other in runs[1:]:
+        for name, x, y in zip(("O", "LSE", "dQ", "dK", "dV", "dQ32", "dK32", "dV32"),
+                              runs[0], other):
+            assert torch.equal(x, y), name
 
 
 # ---------------------------------------------------------------------------
