@@ -301,16 +301,22 @@ int teeny_decode_attention_dev(const void* q, const void* k_cache, const void* v
 int teeny_argmax_rows(const void* x, int64_t* out, int rows, int cols, int dtype,
                       hipStream_t stream);
 
-/* Decode-step linear layer y[M, N] = x[M, K] . w[N, K]^T, bf16 only, for
- * 1 <= M <= 16 (one token per sequence): replaces the external teeny-core
- * Linear behind sym_linear (src/layers/mod.rs:54-58) at the shapes a KV-cached
- * decode step has.  Requires N % 128 == 0 and K % 128 == 0; other shapes return
- * TEENY_ERR_UNSUPPORTED (the caller then uses a general GEMM).  Deterministic.
+/* Linear layer y[M, N] = x[M, K] . w[N, K]^T, bf16 only, any M >= 1: replaces
+ * the external teeny-core Linear behind sym_linear (src/layers/mod.rs:54-58).
+ * Up to 16 rows (a KV-cached decode step) with N % 128 == 0 and K % 128 == 0
+ * stream the weight through a GEMV-shaped kernel; every other shape runs the
+ * matrix-core GEMM, which requires N % 64 == 0 and K % 64 == 0 (otherwise
+ * TEENY_ERR_UNSUPPORTED).  Either path is deterministic, with fp32
+ * accumulation and one bf16 rounding of each output.
  * teeny_linear_swiglu_bf16: w is the fused gate_up weight [2F, K] (gate rows
- * first, src/loader.rs:49-55), F % 64 == 0; writes y[M, F] =
- * silu(x w_gate^T) * (x w_up^T) with both products rounded to bf16 first, as
- * FeedForward's gate_up Linear followed by SwigluOp computes it
- * (src/layers/ffn.rs:47-56). */
+ * first, src/loader.rs:49-55); writes y[M, F] = silu(x w_gate^T) *
+ * (x w_up^T) with both products rounded to bf16 first, as FeedForward's
+ * gate_up Linear followed by SwigluOp computes it (src/layers/ffn.rs:47-56),
+ * without writing the [M, 2F] product: up to 16 rows with F % 64 == 0 and
+ * K % 128 == 0 take the weight-streaming kernel, other shapes the GEMM with
+ * the SwiGLU in its epilogue (F % 32 == 0 and K % 64 == 0, otherwise
+ * TEENY_ERR_UNSUPPORTED).  Bit-identical to teeny_linear_bf16 on [2F, K]
+ * followed by teeny_swiglu_fwd. */
 int teeny_linear_bf16(const void* x, const void* w, void* y, int M, int N, int K,
                       hipStream_t stream);
 int teeny_linear_swiglu_bf16(const void* x, const void* w, void* y, int M, int F, int K,

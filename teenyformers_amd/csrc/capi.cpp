@@ -975,12 +975,23 @@ int teeny_linear_bf16(const void* x, const void* w, void* y, int M, int N, int K
   return launch("teeny_gemm_bf16_nt", dim3(tiles_m * tiles_n), dim3(512), 0, stream, args);
 }
 
+// Any M, as teeny_linear_bf16: up to 16 rows through linear_bf16.hip's
+// weight-streaming kernel when F % 64 and K % 128 are 0; otherwise the GEMM
+// with the SwiGLU epilogue (256 rows x 128 features per workgroup).
 int teeny_linear_swiglu_bf16(const void* x, const void* w, void* y, int M, int F, int K,
                              hipStream_t stream) {
-  int rc = linear_sk_check(x, w, y, M, F, K, 2L * F, 64);
-  if (rc) return rc;
-  void* args[] = {&x, &w, &y, &M, &F, &K};
-  return launch("teeny_linear_sk_swiglu_bf16", dim3(F / 64), dim3(512), 0, stream, args);
+  if (!x || !w || !y) return TEENY_ERR_NULL_POINTER;
+  if (M <= 0 || F <= 0 || K <= 0 || 2L * F * K >= kMaxElems * 2) return TEENY_ERR_INVALID_SHAPE;
+  if (M <= 16 && F % 64 == 0 && K % 128 == 0) {
+    void* args[] = {&x, &w, &y, &M, &F, &K};
+    return launch("teeny_linear_sk_swiglu_bf16", dim3(F / 64), dim3(512), 0, stream, args);
+  }
+  if (F % 32 != 0 || K % 64 != 0) return TEENY_ERR_UNSUPPORTED;
+  if ((long)K * 2 * 256 >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
+  int tiles_m = (M + 255) / 256, tiles_n = (F + 127) / 128;
+  if ((long)tiles_m * tiles_n >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
+  void* args[] = {&x, &w, &y, &M, &F, &K, &tiles_m, &tiles_n};
+  return launch("teeny_gemm_swiglu_bf16_nt", dim3(tiles_m * tiles_n), dim3(512), 0, stream, args);
 }
 
 int teeny_linear_partials_count(int K, int k_split) {

@@ -53,7 +53,13 @@ DEVI int gpos(int r, int c) {
 // (WAVES / WGM along N); GROUP_M: tile-rows per group of the tile order; RA:
 // 16-k steps of fragment read-ahead; IL: the refill's loads are issued IL at a
 // time between the products of the step that issues them (0: all at once).
-template <int BM, int BN, int BK, int NS, int WAVES, int WGM, int GROUP_M, int RA, int IL = 0>
+// SWIGLU: w is a fused gate_up weight [2N, K] (gate rows, then up rows) and
+// y[M, N] = silu(g) * u with g = bf16(x w_gate^T), u = bf16(x w_up^T): the
+// workgroup's BN W rows are BN/2 gate rows and the matching BN/2 up rows,
+// each wavefront's two 32-column blocks a gate block and its up block, so
+// the epilogue holds both factors of every output in one lane.
+template <int BM, int BN, int BK, int NS, int WAVES, int WGM, int GROUP_M, int RA, int IL = 0,
+          bool SWIGLU = false>
 __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const bf16* __restrict__ w,
                              bf16* __restrict__ y, int M, int N, int K, int tiles_m,
                              int tiles_n) {
@@ -91,7 +97,9 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
   const int gm = min(tiles_m - first_m, GROUP_M);
   const int in_grp = id - grp * per_group;
   const int tm = first_m + in_grp % gm, tn = in_grp / gm;
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * BM;
+  const int n0 = tn * (SWIGLU ? BN / 2 : BN);  // first output column
+  static_assert(!SWIGLU || J == 2, "a gate block and an up block per wavefront");
 
   // ---- DMA sources: slot P = j * NT + tid (16 bytes) of a tile holds the
   //      chunk of row r = P / CPR whose position gpos gives.  Load j of a
@@ -101,9 +109,13 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
   //      loads return zeros (no access), and they only feed outputs that
   //      are not stored. ---------------------------------------------------
   static_assert((NT / CPR) % 32 == 0, "row step of the DMA loads keeps the swizzle");
-  const int rows_x = min(BM, M - m0), rows_w = min(BN, N - n0);
+  const int rows_x = min(BM, M - m0);
+  const int rows_w = SWIGLU ? min(BN / 2, N - n0) : min(BN, N - n0);
   const auto xr = make_rsrc(x + (long)m0 * K, rows_x * K * 2);
   const auto wr = make_rsrc(w + (long)n0 * K, rows_w * K * 2);
+  // SWIGLU: the tile's second half of W rows, the up rows of the same features
+  const auto wu = make_rsrc(w + ((long)N + n0) * K, rows_w * K * 2);
+  constexpr int WH = LPW / 2;  // W loads per half tile
   uint32_t src0;
   {
     const int r = tid / CPR;
@@ -117,8 +129,12 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
     for (int j = 0; j < LPX; ++j)
       dma16(xr, smx[buf] + j * NT * 16 + wave * 1024, src0, soff + j * jstride);
 #pragma unroll
-    for (int j = 0; j < LPW; ++j)
-      dma16(wr, smw[buf] + j * NT * 16 + wave * 1024, src0, soff + j * jstride);
+    for (int j = 0; j < LPW; ++j) {
+      if (SWIGLU && j >= WH)
+        dma16(wu, smw[buf] + j * NT * 16 + wave * 1024, src0, soff + (j - WH) * jstride);
+      else
+        dma16(wr, smw[buf] + j * NT * 16 + wave * 1024, src0, soff + j * jstride);
+    }
   };
 
   // ---- fragment read offsets: lane reads row (block + l32), chunk 2 kk + g;
@@ -129,8 +145,11 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
 #pragma unroll
   for (int kk = 0; kk < STEPS; ++kk) {
     xoff[kk] = gpos<BK>(wm * WM + l32, 2 * kk + g);
-    woff[kk] = gpos<BK>(wn * WN + l32, 2 * kk + g);
+    woff[kk] = gpos<BK>(wn * (SWIGLU ? WN / 2 : WN) + l32, 2 * kk + g);
   }
+  // W block j starts JROWS rows after block 0: the next 32 rows, or with
+  // SWIGLU the up rows of the gate block's features (half a tile on)
+  constexpr int JROWS = SWIGLU ? BN / 2 : 32;
 
   f32x16 acc[I][J];
 #pragma unroll
@@ -153,7 +172,7 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
       xa[set][i] = *reinterpret_cast<const u32x4*>(xs + xoff[kk] + i * 32 * ROWB);
 #pragma unroll
     for (int j = 0; j < J; ++j)
-      wb[set][j] = *reinterpret_cast<const u32x4*>(ws + woff[kk] + j * 32 * ROWB);
+      wb[set][j] = *reinterpret_cast<const u32x4*>(ws + woff[kk] + j * JROWS * ROWB);
   };
   // y^T blocks: w rows are the A operand (the 32 rows of a block), x rows
   // the B operand (lane = x row)
@@ -226,6 +245,25 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
     const int m = m0 + wm * WM + i * 32 + l32;
     if (m >= M) continue;
     bf16* yr = y + (long)m * N;
+    if constexpr (SWIGLU) {
+      // the unfused path's arithmetic: both products rounded to bf16, then
+      // silu(g) * u in fp32 and one rounding
+      const int nb = n0 + wn * (WN / 2);
+      if (nb >= N) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float gt = bf2f(f2bf(acc[i][0][4 * q + e]));
+          const float up = bf2f(f2bf(acc[i][1][4 * q + e]));
+          o[e] = gt * (1.0f / (1.0f + expf(-gt))) * up;
+        }
+        *reinterpret_cast<u32x2*>(yr + nb + 8 * q + 4 * g) =
+            u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+      }
+      continue;
+    }
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const int nb = n0 + wn * WN + j * 32;
@@ -246,4 +284,11 @@ __device__ __forceinline__ void gemm_bf16_nt(const bf16* __restrict__ x, const b
 extern "C" __global__ __launch_bounds__(512) void teeny_gemm_bf16_nt(
     const bf16* x, const bf16* w, bf16* y, int M, int N, int K, int tiles_m, int tiles_n) {
   gemm_bf16_nt<256, 256, 64, 2, 8, 2, 4, 2, 1>(x, w, y, M, N, K, tiles_m, tiles_n);
+}
+
+// y[M, F] = silu(x w[:F]^T) * (x w[F:]^T) for w = [gate; up] of shape [2F, K];
+// tiles of 256 rows x 128 features
+extern "C" __global__ __launch_bounds__(512) void teeny_gemm_swiglu_bf16_nt(
+    const bf16* x, const bf16* w, bf16* y, int M, int F, int K, int tiles_m, int tiles_n) {
+  gemm_bf16_nt<256, 256, 64, 2, 8, 2, 4, 2, 1, true>(x, w, y, M, F, K, tiles_m, tiles_n);
 }

@@ -508,14 +508,16 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
 
 
 def linear_swiglu(x: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
-    """swiglu(x w_gate_up^T) (src/layers/ffn.rs:47-56): fused in one kernel for
-    up to 16 bf16 rows, else the GEMM followed by the SwiGLU kernel."""
+    """swiglu(x w_gate_up^T) (src/layers/ffn.rs:47-56) in one launch of
+    teeny_linear_swiglu_bf16 for bf16 without gradients (the weight-streaming
+    kernel up to 16 rows, the GEMM with a SwiGLU epilogue above), bit-identical
+    to the GEMM followed by the SwiGLU kernel, which other cases run."""
     x2 = x.reshape(-1, x.shape[-1])
     N2, K = w_gate_up.shape
     if K != x2.shape[1] or N2 % 2:
         raise ValueError("linear_swiglu: weight must be [2F, in] with in = x's features")
     F = N2 // 2
-    if not _skinny(x2, w_gate_up, F, row_tile=64):
+    if not _gemm(x2, w_gate_up):
         return swiglu(linear(x, w_gate_up))
     x2 = x2.contiguous()
     y = torch.empty((x2.shape[0], F), dtype=x.dtype, device=x.device)

@@ -154,10 +154,15 @@ def test_decode_ops_validation(L):
     assert L.teeny_linear_bf16(P, P, P, 16, 64, 96, None) == UNSUP
     assert L.teeny_linear_bf16(P, P, P, 300, 128, 4100, None) == UNSUP
     assert L.teeny_linear_bf16(P, P, P, 300, 128, 1 << 22, None) == SHAPE  # 32-bit offsets
-    assert L.teeny_linear_swiglu_bf16(P, P, P, 17, 64, 128, None) == UNSUP
+    # linear_swiglu: the GEMM needs F % 32 and K % 64 (the decode kernel,
+    # M <= 16, F % 64 and K % 128)
+    assert L.teeny_linear_swiglu_bf16(P, P, P, 17, 48, 128, None) == UNSUP
+    assert L.teeny_linear_swiglu_bf16(P, P, P, 300, 64, 96, None) == UNSUP
+    assert L.teeny_linear_swiglu_bf16(P, P, P, 300, 64, 1 << 22, None) == SHAPE
+    assert L.teeny_linear_swiglu_bf16(P, None, P, 300, 64, 128, None) == NULLP
     assert L.teeny_linear_bf16(None, P, P, 16, 128, 128, None) == NULLP
     assert L.teeny_linear_bf16(P, P, P, 0, 128, 128, None) == SHAPE
-    assert L.teeny_linear_swiglu_bf16(P, P, P, 4, 32, 128, None) == UNSUP
+    assert L.teeny_linear_swiglu_bf16(P, P, P, 4, 48, 128, None) == UNSUP
     assert L.teeny_linear_partials_bf16(P, P, P, 4, 128, 4096, 1000, None) == VALUE
     assert L.teeny_linear_partials_bf16(P, P, P, 4, 128, 4096, 0, None) == VALUE
     assert L.teeny_linear_partials_count(4096, 1024) == 4

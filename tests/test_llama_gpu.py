@@ -382,3 +382,27 @@ def test_linear_swiglu_skinny(cuda, M, F, K):
     # one bf16 step of z can move silu(g) * u by a few output ulps
     assert np.all(err <= np.abs(want) * 2.0 ** -5 + 1e-3 * np.abs(want).max()), err.max()
     assert rel_l2(host(y), want) <= 5e-3
+
+
+@pytest.mark.parametrize("M,F,K", [
+    (8192, 1792, 4096),   # Llama-3-8B's MLP on 16 x 512 tokens, an eighth of its features
+    (300, 96, 640),       # a ragged row tile; the feature tile three quarters full
+    (17, 160, 128),       # one 64-deep K tile; a second feature tile of 32
+    (5, 32, 192),         # few rows, F % 64 != 0: the GEMM, not the decode kernel
+    (16, 448, 4096)])     # the decode kernel
+def test_linear_swiglu_any_rows(cuda, M, F, K):
+    """teeny_linear_swiglu_bf16 at any M gives the bits of the unfused
+    composition (the GEMM on the [2F, K] weight, then the SwiGLU kernel), and
+    that composition is within the bf16 tolerance of the float64 product."""
+    rng = np.random.default_rng(M + 3 * F + K)
+    x = _bf16_dev(rng.standard_normal((M, K)).astype(np.float32))
+    w = _bf16_dev((0.02 * rng.standard_normal((2 * F, K))).astype(np.float32))
+    y = ops.linear_swiglu(x, w)
+    z = ops.linear(x, w)
+    assert torch.equal(y, ops.swiglu(z))
+    assert torch.equal(y, ops.linear_swiglu(x, w))  # deterministic
+    if M * F <= 1 << 20:
+        xh, wh = host(x).astype(np.float64), host(w).astype(np.float64)
+        zh = O.bf16_round((xh @ wh.T).astype(np.float32))
+        want = O.bf16_round(O.swiglu_fwd(zh))
+        assert rel_l2(host(y), want) <= 5e-3
