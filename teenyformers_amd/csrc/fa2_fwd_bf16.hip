@@ -28,8 +28,12 @@
 //     row max and exponentials of tile i (fenced issue order), so the matrix
 //     cores and the VALU work at once within one wave;
 //   * online softmax in the log2 domain (exp2 with log2(e) folded into the
-//     scale) with a lazy, branch-free maximum update: O is rescaled only when
-//     some row's maximum grew by more than 2^8;
+//     scale) without a per-tile maximum: the exponent offset is the row's
+//     maximum over its first key tile, and a later tile's P = 2^(t - m) is
+//     only checked afterwards through its row sums (any partial sum at or
+//     above 2^31, or not finite, redoes the tile with its maximum and
+//     rescales O and l); P, l and O stay far from fp32 overflow, and the
+//     floating-point results are scale-invariant;
 //   * causal: key tiles past the block's last row are not loaded, diagonal
 //     tiles are masked;
 //   * GQA: q head h reads kv head h / (Hq / Hkv);
@@ -47,7 +51,7 @@ constexpr int KBUF = 2;  // K tiles in flight: read by QK(i), loading i+1
 constexpr int VBUF = 3;  // V tiles: read by PV(i-1), waiting (i), loading (i+1)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr float kRescale = 8.0f;  // lazy-rescale threshold, log2 units
+constexpr float kPmax = 2147483648.0f;  // 2^31: a tile's partial row sums stay below
 
 template <int D>
 struct __attribute__((aligned(16))) FwdSmem {
@@ -109,26 +113,17 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   const uint32_t v_src = swz<SWZ_DUAL, D>(wave * 64 + lane) * 16;
   const auto krsrc = make_rsrc(kb, nk * D * 2);
   const auto vrsrc = make_rsrc(vb, nk * D * 2);
-  // it: tile index; koff / voff: byte offsets of its K and V buffers
+  // it: tile index; koff / voff: byte offsets of its K and V buffers.  Rows
+  // past the sequence lie outside the descriptors' ranges and load as zeros:
+  // their scores are masked, and P = 0 times V = 0 adds nothing.
   auto load_tile = [&](int it, int koff, int voff) {
-    const int kbase = it * BN;
     char* kdst = sm.k[0] + koff + wave * 64 * 16;
     char* vdst = sm.v[0] + voff + wave * 64 * 16;
-    const int sbase = kbase * D * 2;
-    if (kbase + BN <= nk) {
+    const int sbase = it * BN * D * 2;
 #pragma unroll
-      for (int i = 0; i < TCH; ++i) {
-        dma16(krsrc, kdst + i * 4096, k_src, sbase + i * 4096);
-        dma16(vrsrc, vdst + i * 4096, v_src, sbase + i * 4096);
-      }
-    } else {  // rows past the sequence re-read its last row (masked later)
-      const int last = nk - 1 - kbase;
-#pragma unroll
-      for (int i = 0; i < TCH; ++i) {
-        const int ko = i * 4096 + k_src, vo = i * 4096 + v_src;
-        dma16(krsrc, kdst + i * 4096, min(ko / (2 * D), last) * (2 * D) + ko % (2 * D), sbase);
-        dma16(vrsrc, vdst + i * 4096, min(vo / (2 * D), last) * (2 * D) + vo % (2 * D), sbase);
-      }
+    for (int i = 0; i < TCH; ++i) {
+      dma16(krsrc, kdst + i * 4096, k_src, sbase + i * 4096);
+      dma16(vrsrc, vdst + i * 4096, v_src, sbase + i * 4096);
     }
   };
 
@@ -162,9 +157,8 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   f32x16 acc_o[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc_o[t] = f32x16{};
-  // m_run is raised lazily: only when some row of the wave sees a max more
-  // than kRescale above it are O and l rescaled, so p = 2^(t - m_run) stays
-  // below 2^kRescale (exact in fp32 and representable in bf16).
+  // m_run: the exponent offset of P, the row maximum of the first tile,
+  // raised only by a tile whose P would reach 2^31 (then O and l rescale)
   float m_run = -INFINITY;
   // this lane's partial row sums (its 16 of every 32 keys), two chains
   float l_run = 0.0f, l_run2 = 0.0f;
@@ -234,11 +228,10 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
     }
   };
 
-  // Row max of a tile in four pieces (so that they can sit between matrix
-  // products), the last one followed by the branch-free online-softmax
-  // update: grow = some row of the wave raised its maximum by more than
-  // kRescale (O must then be scaled by alpha before the next product), m_run
-  // and the row sums updated, m_use the exponent offset for this tile's P.
+  // Row max of a tile in four pieces, the last one followed by the online-
+  // softmax update (first tile, or a tile redone): m_run raised to the
+  // tile's maximum where that is larger, alpha the factor of O and l (O is
+  // scaled before the next product: grow), m_use the exponent offset of P.
   float mxa, mxb, alpha = 1.0f, m_use = 0.0f;
   bool grow = false;
   auto max_piece = [&](int u, const f32x16& s0, const f32x16& s1) {
@@ -255,39 +248,44 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
       float mx = max3(mxa, mxb, max3(s0[15], s1[15], s1[15]));
       mx = max3(mx, other_half(mx), mx);
       const float m_tile = mx * sl2;  // scale > 0, so max(scale*s) = scale*max(s)
-      grow = __any(m_tile > m_run + kRescale);
-      if (grow) {  // wave-uniform: most tiles skip the update
-        const float m_new = fmaxf(m_run, m_tile);
-        // 0 on a row's first tile; exactly 1 where the maximum is unchanged
-        alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
-        m_run = m_new;
-        l_run *= alpha;
-        l_run2 *= alpha;
-        m_use = m_run == -INFINITY ? 0.0f : m_run;
-      }
+      const float m_new = fmaxf(m_run, m_tile);
+      // 0 on a row's first tile; exactly 1 where the maximum is unchanged
+      alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+      l_run2 *= alpha;
+      m_use = m_run == -INFINITY ? 0.0f : m_run;
+      grow = true;
     }
   };
-  // softmax of element pair q (0..15): half q%2 (s0 / s1), rows 2(q/2), +1
-  auto sm_pair = [&](const f32x16& s0, const f32x16& s1, float m_use, int q) {
+  // softmax of element pair q (0..15): half q%2 (s0 / s1), rows 2(q/2), +1;
+  // the row sums (la: s0's keys, lb: s1's) add the bf16 P that the PV
+  // product consumes
+  auto sm_pair = [&](const f32x16& s0, const f32x16& s1, int q, float& la, float& lb) {
     const int hf = q & 1, r = (q >> 1) * 2;
     const float x0 = hf ? s1[r] : s0[r], x1 = hf ? s1[r + 1] : s0[r + 1];
     const uint32_t w = pack_bf16x2(fast_exp2(__builtin_fmaf(x0, sl2, -m_use)),
                                    fast_exp2(__builtin_fmaf(x1, sl2, -m_use)));
     pnew[hf][r >> 1] = w;
-    // the row sum adds the bf16 P that the PV product consumes
-    if (hf) l_run2 = add_bf16x2(w, l_run2);
-    else l_run = add_bf16x2(w, l_run);
+    if (hf) lb = add_bf16x2(w, lb);
+    else la = add_bf16x2(w, la);
   };
-  // VALU work of one tile = 20 units: 4 row-max pieces, then 16 softmax pairs
-  auto run_unit = [&](int u, const f32x16& s0, const f32x16& s1) {
-    if (u < 4) max_piece(u, s0, s1);
-    else sm_pair(s0, s1, m_use, u - 4);
+  // the tile's partial row sums are checked before they join l: a tile with
+  // a sum at or above 2^31 (or not finite) is redone with its maximum
+  auto check_tile = [&](const f32x16& s0, const f32x16& s1, float& la, float& lb) {
+    if (__any(!(fmaxf(la, lb) < kPmax))) {  // wave-uniform and rare
+#pragma unroll
+      for (int u = 0; u < 4; ++u) max_piece(u, s0, s1);
+      la = 0.0f;
+      lb = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) sm_pair(s0, s1, q, la, lb);
+    }
+    l_run += la;
+    l_run2 += lb;
   };
-  // the product after which unit u is issued (NJ = 16 or 8 products)
-  auto unit_slot = [](int u) {
-    if (NJ == 16) return u < 4 ? u : (u - 4 < 8 ? 4 + (u - 4) / 2 : u - 4);
-    return u < 4 ? u / 2 : (u - 4 < 12 ? 2 + (u - 4) / 3 : 6 + (u - 16) / 2);
-  };
+  // the product after which softmax pair q is issued (NJ = 16 or 8 products)
+  auto pair_slot = [](int q) { return q * NJ / 16; };
   auto rescale_o = [&]() {
 #pragma unroll
     for (int t = 0; t < DT; ++t) acc_o[t] *= alpha;
@@ -304,7 +302,10 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
     qk(sm.k[0], s0, s1);
     mask(0, s0, s1);
 #pragma unroll
-    for (int u = 0; u < 20; ++u) run_unit(u, s0, s1);  // O is still zero: no scaling due
+    for (int u = 0; u < 4; ++u) max_piece(u, s0, s1);
+    grow = false;  // O is still zero: no scaling due
+#pragma unroll
+    for (int q = 0; q < 16; ++q) sm_pair(s0, s1, q, l_run, l_run2);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       pprev[0][i] = pnew[0][i];
@@ -328,10 +329,14 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
     qk(sm.k[kb], s0, s1);
     mask(kbase, s0, s1);
     // a maximum raised by tile it-1 scales O before tile it-1's product
-    if (grow) rescale_o();
+    if (grow) {
+      rescale_o();
+      grow = false;
+    }
+    float la = 0.0f, lb = 0.0f;
 
     // issue order, fenced: V reads VPF products ahead; each product followed
-    // by its share of the VALU work (row max first, then the exponentials).
+    // by its share of the exponentials.
     // Tile it+1's loads go out halfway through the PV products: issued
     // before the score products they held up the first MFMAs; issued right
     // after them, a quarter or three quarters of the way through the PV
@@ -345,12 +350,13 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
       if (j + VPF < NJ) va[j + VPF] = pv_read(vt, j + VPF);
       pv_mfma(j, va[j]);
 #pragma unroll
-      for (int u = 0; u < 20; ++u)
-        if (unit_slot(u) == j) run_unit(u, s0, s1);
+      for (int q = 0; q < 16; ++q)
+        if (pair_slot(q) == j) sm_pair(s0, s1, q, la, lb);
       if (j == NJ / 2 && it + 1 < n_iter)
         load_tile(it + 1, ((kb + 1) % KBUF) * TILE, ((vp + 2) % VBUF) * TILE);
       __builtin_amdgcn_sched_barrier(0);
     }
+    check_tile(s0, s1, la, lb);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       pin(pnew[0][i]);
