@@ -156,6 +156,27 @@ def test_fa2_bf16_fwd(cuda, shape, causal):
     assert np.abs(host(lse) - le).max() <= 2e-2
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_fa2_bf16_fwd_late_maximum(cuda, causal):
+    """Rows whose maximum score lies far past their first 64-key tile: keys
+    150-159 scaled x30 and key 300 x60 put P = 2^(t - m) of the first tile's
+    maximum m beyond 2^31 (and beyond fp32 for key 300), so the forward must
+    redo those tiles with their own maximum and rescale O and l; O and LSE
+    as the oracle's."""
+    B, Hq, Hkv, S, D = 1, 4, 2, 384, 128
+    q, k, v, _ = inputs(31, B, Hq, Hkv, S, S, D, bf16=True)
+    k[:, :, 150:160] *= 30
+    k[:, :, 300] *= 60
+    k = O.bf16_round(k)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = ops.flash_attn2_fwd(dev(q, torch.bfloat16), dev(k, torch.bfloat16),
+                                 dev(v, torch.bfloat16), scale, causal)
+    oe, le = O.fa2_fwd(q, k, v, scale, causal)
+    assert np.isfinite(host(o)).all() and np.isfinite(host(lse)).all()
+    check_bf16("O", host(o), oe)
+    assert np.abs(host(lse) - le).max() <= 2e-2 * max(1.0, float(np.abs(le).max()) / 64)
+
+
 @pytest.mark.parametrize("shape", BF16_SHAPES)
 @pytest.mark.parametrize("causal", [True, False])
 def test_fa2_bf16_bwd(cuda, shape, causal):
