@@ -9,7 +9,9 @@
 //
 // Tiling (one workgroup = 4 wavefronts = 128 query rows of one (b, h); two
 // workgroups per CU, so the two waves on each SIMD run independently and
-// cover each other's MFMA / VALU phases):
+// cover each other's MFMA / VALU phases.  Long GQA sequences take the _w8
+// form: 8 wavefronts = 256 rows share each K/V tile, one workgroup per CU,
+// half the L2 -> LDS traffic per product):
 //   * each wave owns 32 query rows; its Q rows live in registers as the
 //     B operand of v_mfma_f32_32x32x16_bf16;
 //   * K/V advance in tiles of 64 keys that buffer_load ... lds streams into
@@ -45,7 +47,6 @@
 
 namespace {
 
-constexpr int BM = 128;  // query rows per workgroup
 constexpr int BN = 64;   // keys per iteration
 constexpr int KBUF = 2;  // K tiles in flight: read by QK(i), loading i+1
 constexpr int VBUF = 3;  // V tiles: read by PV(i-1), waiting (i), loading (i+1)
@@ -59,15 +60,19 @@ struct __attribute__((aligned(16))) FwdSmem {
   char v[VBUF][BN * D * 2];
 };
 
-template <int D, bool CAUSAL>
+// NW wavefronts (4 or 8) of 32 query rows each
+template <int D, bool CAUSAL, int NW = 4>
 __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict__ k,
                              const bf16* __restrict__ v, bf16* __restrict__ o,
                              float* __restrict__ lse, int nq, int nk, float scale, int hq, int hkv,
                              int num_m_blocks, int total_blocks) {
+  constexpr int BM = 32 * NW;          // query rows per workgroup
+  constexpr int NT = 64 * NW;          // threads
   constexpr int DC = D / 16;           // d-chunks of 16 for QK^T
   constexpr int DT = D / 32;           // d-tiles of 32 for PV
   constexpr int CPR = D / 8;           // 16-byte chunks per row
-  constexpr int TCH = BN * CPR / 256;  // chunks per thread per tile (K and V each)
+  constexpr int TCH = BN * CPR / NT;   // chunks per thread per tile (K and V each)
+  constexpr int LSTEP = NT * 16;       // bytes of one load across the workgroup
   constexpr int TILE = BN * D * 2;     // bytes per tile
   __shared__ FwdSmem<D> sm;
 
@@ -106,9 +111,9 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   // buffer_load ... lds (MUBUF, not FLAT: LDS waits elsewhere in the loop keep
   // partial counts), address = SGPR descriptor of the head + SGPR tile offset
   // + one VGPR per lane.  Load i of a wave writes LDS chunks
-  // (i*256 + wave*64 + lane) of the tile; each lane fetches the tile chunk
+  // (i*NT + wave*64 + lane) of the tile; each lane fetches the tile chunk
   // that the swizzle puts there.  Adding 256 chunks (16 lines) leaves both
-  // swizzles unchanged, so a lane's chunks are one byte offset plus i * 4096.
+  // swizzles unchanged, so a lane's chunks are one byte offset plus i * LSTEP.
   const uint32_t k_src = swz<SWZ_ROW, D>(wave * 64 + lane) * 16;
   const uint32_t v_src = swz<SWZ_DUAL, D>(wave * 64 + lane) * 16;
   const auto krsrc = make_rsrc(kb, nk * D * 2);
@@ -122,8 +127,8 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
     const int sbase = it * BN * D * 2;
 #pragma unroll
     for (int i = 0; i < TCH; ++i) {
-      dma16(krsrc, kdst + i * 4096, k_src, sbase + i * 4096);
-      dma16(vrsrc, vdst + i * 4096, v_src, sbase + i * 4096);
+      dma16(krsrc, kdst + i * LSTEP, k_src, sbase + i * LSTEP);
+      dma16(vrsrc, vdst + i * LSTEP, v_src, sbase + i * LSTEP);
     }
   };
 
@@ -434,3 +439,14 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
 
 TEENY_FA2_FWD_BF16_INST(64)
 TEENY_FA2_FWD_BF16_INST(128)
+
+// 8 wavefronts, 256 query rows per workgroup (long GQA sequences)
+#define TEENY_FA2_FWD_BF16_W8_INST(D, C, CZ)                                                    \
+  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
+  void teeny_fa2_fwd_bf16_d##D##_##CZ##_w8(                                                      \
+      const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,            \
+      float scale, int hq, int hkv, int nmb, int total) {                                        \
+    fa2_fwd_bf16<D, C, 8>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);                    \
+  }
+TEENY_FA2_FWD_BF16_W8_INST(128, true, c)
+TEENY_FA2_FWD_BF16_W8_INST(128, false, n)
