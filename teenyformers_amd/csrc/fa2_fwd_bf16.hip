@@ -106,6 +106,9 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   int kend = nk;
   if (CAUSAL) kend = min(nk, m0 + BM);
   const int n_iter = (kend + BN - 1) / BN;
+  // causal: the workgroup's tiles past this wavefront's last row are fully
+  // masked for it; it computes only the first n_live (wave-uniform)
+  const int n_live = CAUSAL ? min(n_iter, wave_qmax / BN + 1) : n_iter;
 
   // ---- direct global -> LDS tile loads --------------------------------------
   // buffer_load ... lds (MUBUF, not FLAT: LDS waits elsewhere in the loop keep
@@ -379,7 +382,7 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     int it = 1;
-    for (; it + 6 <= n_iter; it += 6) {
+    for (; it + 6 <= n_live; it += 6) {
       tile_step(it, I1{}, I0{});
       tile_step(it + 1, I0{}, I1{});
       tile_step(it + 2, I1{}, I2{});
@@ -387,18 +390,27 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
       tile_step(it + 4, I1{}, I1{});
       tile_step(it + 5, I0{}, I2{});
     }
-    // the last (n_iter - 1) % 6 tiles (same buffer sequence)
-    if (it < n_iter) tile_step(it, I1{}, I0{});
-    if (it + 1 < n_iter) tile_step(it + 1, I0{}, I1{});
-    if (it + 2 < n_iter) tile_step(it + 2, I1{}, I2{});
-    if (it + 3 < n_iter) tile_step(it + 3, I0{}, I0{});
-    if (it + 4 < n_iter) tile_step(it + 4, I1{}, I1{});
+    // the last (n_live - 1) % 6 tiles (same buffer sequence)
+    if (it < n_live) tile_step(it, I1{}, I0{});
+    if (it + 1 < n_live) tile_step(it + 1, I0{}, I1{});
+    if (it + 2 < n_live) tile_step(it + 2, I1{}, I2{});
+    if (it + 3 < n_live) tile_step(it + 3, I0{}, I0{});
+    if (it + 4 < n_live) tile_step(it + 4, I1{}, I1{});
   }
   if (n_iter > 0) {
     if (grow) rescale_o();
-    const char* vt = sm.v[0] + ((n_iter - 1) % VBUF) * TILE;  // tile n_iter-1's V
+    const char* vt = sm.v[0] + ((n_live - 1) % VBUF) * TILE;  // tile n_live-1's V
 #pragma unroll
     for (int j = 0; j < NJ; ++j) pv_mfma(j, pv_read(vt, j));
+    // a wavefront whose rows end before the workgroup's last tiles still
+    // loads its share of them and meets the workgroup at each of their
+    // barriers (tile t + 1 goes to K buffer (t + 1) % 2, V buffer (t + 1) % 3,
+    // as in the steps)
+    for (int t = n_live; t < n_iter; ++t) {
+      if (t + 1 < n_iter) load_tile(t + 1, ((t + 1) % KBUF) * TILE, ((t + 1) % VBUF) * TILE);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
   }
 
   // ---- epilogue ----
