@@ -500,6 +500,9 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   int kend = nk;
   if (CAUSAL) kend = min(nk, m0 + QBM);
   const int n_iter = (kend + QBN - 1) / QBN;
+  // causal: the workgroup's tiles past this wavefront's last row are fully
+  // masked for it; it computes only the first n_live (wave-uniform)
+  const int n_live = CAUSAL ? min(n_iter, (m0 + wave * 32 + 31) / QBN + 1) : n_iter;
 
   // ---- K / V tiles: buffer_load ... lds, both SWZ_DUAL ----------------------
   const uint32_t src = swz<SWZ_DUAL, D>(wave * 64 + lane) * 16;
@@ -685,7 +688,7 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   int it = 0;
-  for (; it + 6 <= n_iter; it += 6) {
+  for (; it + 6 <= n_live; it += 6) {
     tile_step(it, I0{}, I0{});
     tile_step(it + 1, I1{}, I1{});
     tile_step(it + 2, I2{}, I0{});
@@ -693,16 +696,24 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
     tile_step(it + 4, I1{}, I0{});
     tile_step(it + 5, I2{}, I1{});
   }
-  // the last n_iter % 6 tiles (same buffer sequence)
-  if (it < n_iter) tile_step(it, I0{}, I0{});
-  if (it + 1 < n_iter) tile_step(it + 1, I1{}, I1{});
-  if (it + 2 < n_iter) tile_step(it + 2, I2{}, I0{});
-  if (it + 3 < n_iter) tile_step(it + 3, I0{}, I1{});
-  if (it + 4 < n_iter) tile_step(it + 4, I1{}, I0{});
-  if (n_iter > 0) {  // tile n_iter-1's second half: its dS^T product is pending
-    const char* kl = sm.k[0] + ((n_iter - 1) % QKBUF) * TILE + HALF;
+  // the last n_live % 6 tiles (same buffer sequence)
+  if (it < n_live) tile_step(it, I0{}, I0{});
+  if (it + 1 < n_live) tile_step(it + 1, I1{}, I1{});
+  if (it + 2 < n_live) tile_step(it + 2, I2{}, I0{});
+  if (it + 3 < n_live) tile_step(it + 3, I0{}, I1{});
+  if (it + 4 < n_live) tile_step(it + 4, I1{}, I0{});
+  if (n_iter > 0) {  // tile n_live-1's second half: its dS^T product is pending
+    const char* kl = sm.k[0] + ((n_live - 1) % QKBUF) * TILE + HALF;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) dq_mfma(j, dq_read(kl, j));
+    // a wavefront whose rows end before the workgroup's last tiles still
+    // loads its share of them and meets the workgroup at each of their
+    // barriers (tile t + 1 goes to K buffer (t + 1) % 3, V buffer (t + 1) % 2)
+    for (int t = n_live; t < n_iter; ++t) {
+      if (t + 1 < n_iter) load_tile(t + 1, ((t + 1) % QKBUF) * TILE, ((t + 1) % QVBUF) * TILE);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
   }
 
   if (qok) {
