@@ -302,10 +302,18 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
 
   // ---- first tile: scores and P only ----
   if (n_iter > 0) {
+    // tile 1 is requested with tile 0, before the first wait: its latency
+    // overlaps the first tile's, and the first tile's products wait only for
+    // the Q rows and tile 0 (tile 1's 2 TCH loads, issued last, may still fly)
     load_tile(0, 0, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (n_iter > 1) load_tile(1, TILE, TILE);
+    if (n_iter > 1) {
+      load_tile(1, TILE, TILE);
+      __builtin_amdgcn_s_waitcnt(kVmWaitLgkm0<2 * TCH>());
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    // (the barrier alone: __syncthreads would wait for tile 1's loads too)
+    barrier_only();
     f32x16 s0, s1;
     qk(sm.k[0], s0, s1);
     mask(0, s0, s1);
