@@ -661,9 +661,17 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   // zero it (buffer QKBUF-1, second half) so that 0 * K stays 0.
   for (int i = tid; i < HALF / 16; i += 256)
     *reinterpret_cast<u32x4*>(sm.k[QKBUF - 1] + HALF + 16 * i) = u32x4{0, 0, 0, 0};
+  // tile 1 is requested with tile 0, before the first wait (its latency
+  // overlaps tile 0's); the barrier alone, since __syncthreads would wait
+  // for tile 1's loads too
   if (n_iter > 0) load_tile(0, 0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  if (n_iter > 1) {
+    load_tile(1, TILE, TILE);
+    __builtin_amdgcn_s_waitcnt(kVmWaitLgkm0<2 * TCH>());
+  } else {
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+  barrier_only();
 
   // Tile it uses K buffer it % 3 and V buffer it % 2.  The loop is unrolled
   // over the 6 tiles after which both rotations repeat, so every LDS address
@@ -675,7 +683,7 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
     for (int u = 0; u < 2; ++u) {
       f32x16 s, dp;
       s_dp(sm.k[kb] + u * HALF, sm.v[vb] + u * HALF, s, dp);
-      if (u == 0 && it + 1 < n_iter)  // after the first products (as in the forward)
+      if (u == 0 && it > 0 && it + 1 < n_iter)  // after the first products (as in the forward)
         load_tile(it + 1, ((kb + 1) % QKBUF) * TILE, ((vb + 1) % QVBUF) * TILE);
       mask(it * QBN + 32 * u, s);
       // the pending dS^T is of the previous half: tile it-1's second half, then this tile's first
