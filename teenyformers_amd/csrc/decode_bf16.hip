@@ -186,15 +186,17 @@ __device__ void decode_mfma(const bf16* __restrict__ q, const bf16* __restrict__
 //   1. the group's q heads and the kv head's k, v rows are summed from the
 //      QKV projection's K-split slabs (in slab order, rounded to bf16 as the
 //      unsplit product is stored), RoPE is applied at position n_past to q
-//      and k (qkv_rope_split's arithmetic), k and v are written to the cache
-//      row n_past and q is kept in LDS;
+//      and k (qkv_rope_split's arithmetic); q, k and v stay in LDS;
 //   2. the cache rows 0 .. min(n_past + 1, cache_len) - 1 are split between
 //      the 8 wavefronts, each running decode_mfma's loop on its own LDS
-//      buffer of one 32-key tile (a wavefront's first tile, unless it holds
-//      row n_past, is requested before step 1, so the two latencies
-//      overlap);
+//      buffer of one 32-key tile.  Every wavefront's first tile is requested
+//      before step 1, so the two latencies overlap; the cache is read only
+//      below row n_past (rows at or past it load as zeros: outside the
+//      descriptors' ranges) and the wavefront whose tile holds row n_past
+//      copies the new k, v row from LDS into it;
 //   3. the 8 partials (max, sum, unnormalised O) are merged in LDS and
-//      o [B, Hq, D] is stored.
+//      o [B, Hq, D] is stored, and the new k, v row is written to the cache
+//      (row n_past, when it is below cache_len) for the next steps.
 // It replaces the QKV split, the split-K decode kernel and the combine
 // kernel of the unfused path with one launch and no partials in HBM.
 constexpr int kDqWaves = 8;
@@ -213,6 +215,7 @@ struct __attribute__((aligned(16))) DecQkvSmem {
     } c;
   } u;
   bf16 q[32 * D];  // the group's RoPE'd q rows
+  bf16 kv[2][D];   // the new cache row: k (RoPE'd), v
 };
 
 template <int D>
@@ -240,39 +243,29 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
   const int k0 = wave * kpw;
   const int k1 = min(k0 + kpw, n_keys);
   const int n_tiles = k0 < k1 ? (k1 - k0 + TK - 1) / TK : 0;
-  const auto krs = make_rsrc(kc + (long)kvh * cache_len * D, cache_len * D * 2);
-  const auto vrs = make_rsrc(vc + (long)kvh * cache_len * D, cache_len * D * 2);
+  // the cache up to row pos - 1 (the rows this step reads from it); rows at
+  // or past pos lie outside the ranges and load as zeros
+  const int rows_old = max(0, min(pos, cache_len));
+  const auto krs = make_rsrc(kc + (long)kvh * cache_len * D, rows_old * D * 2);
+  const auto vrs = make_rsrc(vc + (long)kvh * cache_len * D, rows_old * D * 2);
   uint32_t ksrc[NLD], vsrc[NLD];
 #pragma unroll
   for (int i = 0; i < NLD; ++i) {
     ksrc[i] = swz<SWZ_ROW, D>(i * 64 + lane) * 16;
     vsrc[i] = swz<SWZ_DUAL, D>(i * 64 + lane) * 16;
   }
-  // keys t0 .. t0+TK-1; rows at or past n_keys re-read row n_keys - 1 (masked)
+  // keys t0 .. t0+TK-1 (those at or past n_keys are masked)
   auto load = [&](int t0) {
     const int soff = __builtin_amdgcn_readfirstlane(t0 * D * 2);
     char* kd = sm.u.t.k[wave];
     char* vd = sm.u.t.v[wave];
-    if (t0 + TK <= n_keys) {
 #pragma unroll
-      for (int i = 0; i < NLD; ++i) {
-        dma16(krs, kd + i * 1024, ksrc[i], soff);
-        dma16(vrs, vd + i * 1024, vsrc[i], soff);
-      }
-    } else {
-      const int lastrow = n_keys - 1 - t0;
-#pragma unroll
-      for (int i = 0; i < NLD; ++i) {
-        dma16(krs, kd + i * 1024,
-              min((int)ksrc[i] / (2 * D), lastrow) * (2 * D) + ksrc[i] % (2 * D), soff);
-        dma16(vrs, vd + i * 1024,
-              min((int)vsrc[i] / (2 * D), lastrow) * (2 * D) + vsrc[i] % (2 * D), soff);
-      }
+    for (int i = 0; i < NLD; ++i) {
+      dma16(krs, kd + i * 1024, ksrc[i], soff);
+      dma16(vrs, vd + i * 1024, vsrc[i], soff);
     }
   };
-  // the first tile goes out now unless it holds row pos (written below)
-  const bool early = n_tiles > 0 && k0 + TK <= pos;
-  if (early) load(k0);
+  if (n_tiles > 0) load(k0);
 
   // ---- 1. q, k, v of position pos -------------------------------------------
   const float c = (-2.0f * ln_base) / (float)D;
@@ -297,17 +290,13 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
 #pragma unroll
       for (int j = 0; j < VN; ++j) out[j] = in[j];
     }
-    if (hh < group) {
-      Vec16<bf16>::store(sm.q + hh * D + vv * VN, out);
-    } else if (pos >= 0 && pos < cache_len) {
-      bf16* cache = hh == group ? kc : vc;
-      Vec16<bf16>::store(cache + ((long)kvh * cache_len + pos) * D + vv * VN, out);
-    }
+    if (hh < group) Vec16<bf16>::store(sm.q + hh * D + vv * VN, out);
+    else Vec16<bf16>::store(sm.kv[hh - group] + vv * VN, out);
   }
-  // the new cache row has reached memory (the barrier waits for every
-  // store), so this workgroup's tile loads below read it
-  __syncthreads();
-  if (n_tiles > 0 && !early) load(k0);
+  // q and the new k, v row are in LDS; the barrier alone (no wait for the
+  // tile loads in flight)
+  __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
+  barrier_only();
 
   bf16x8 qreg[DC];
 #pragma unroll
@@ -340,6 +329,19 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
   for (int it = 0; it < n_tiles; ++it) {
     const int t0 = k0 + it * TK;
     __builtin_amdgcn_s_waitcnt(kVmcnt0);  // tile it has landed
+    if (t0 <= pos && pos < t0 + TK) {
+      // the tile holding row pos: its k, v row from LDS (tile chunk
+      // r * CPR + c sits at LDS chunk swz(r * CPR + c)); the reads below are
+      // issued after these writes by the same wavefront
+      if (lane < 2 * CPR) {
+        const int c = lane % CPR, r = pos - t0;
+        const bool isv = lane >= CPR;
+        const u32x4 w = *reinterpret_cast<const u32x4*>(sm.kv[isv] + 8 * c);
+        char* dst = isv ? (char*)vt + swz<SWZ_DUAL, D>(r * CPR + c) * 16
+                        : (char*)kt + swz<SWZ_ROW, D>(r * CPR + c) * 16;
+        *reinterpret_cast<u32x4*>(dst) = w;
+      }
+    }
     u32x4 kr[DC];
 #pragma unroll
     for (int cc = 0; cc < DC; ++cc) kr[cc] = *reinterpret_cast<const u32x4*>(kt + k_off[cc]);
@@ -417,6 +419,13 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
       den += e * sm.u.c.l[w][hh];
     }
     o[((long)b * hq + hk * group + hh) * D + d] = (bf16)(num / den);
+  }
+  // the new k, v row to the cache, for the next steps
+  if (pos >= 0 && pos < cache_len && tid < 2 * CPR) {
+    const int c = tid % CPR;
+    bf16* cache = tid < CPR ? kc : vc;
+    *reinterpret_cast<u32x4*>(cache + ((long)kvh * cache_len + pos) * D + 8 * c) =
+        *reinterpret_cast<const u32x4*>(sm.kv[tid >= CPR] + 8 * c);
   }
 }
 

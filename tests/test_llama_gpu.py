@@ -251,8 +251,8 @@ def test_decode_qkv_attention_fused(cuda, B, Hq, Hkv, D, L):
     """The one-launch decode step (QKV split + RoPE + cache write +
     attention) writes the same cache rows as teeny_qkv_rope_split_partials_dev
     (bit for bit) and its output matches the oracle's attention of that q
-    over the cache rows 0 .. pos; rows past pos hold NaN and are not read; a
-    position past the cache writes nothing."""
+    over the cache rows 0 .. pos (row pos being the new k, v); rows past pos
+    hold NaN and are not read; a position past the cache writes nothing."""
     rng = np.random.default_rng(B * 131 + Hq + D + L)
     d = 512
     n = (Hq + 2 * Hkv) * D
@@ -263,7 +263,9 @@ def test_decode_qkv_attention_fused(cuda, B, Hq, Hkv, D, L):
     kc0 = _bf16_dev(rng.standard_normal((B, Hkv, L, D)).astype(np.float32))
     vc0 = _bf16_dev(rng.standard_normal((B, Hkv, L, D)).astype(np.float32))
     scale = 1.0 / math.sqrt(D)
-    for pos in (0, 37 % L, L - 1, L):
+    # row pos at a tile's first and last key, in a wavefront's first and a
+    # later tile, the last cache row, and past the cache
+    for pos in (0, 31, 32, 37 % L, 300 % L, L - 1, L):
         kc, vc = kc0.clone(), vc0.clone()
         kc[:, :, pos + 1:] = float("nan")
         vc[:, :, pos + 1:] = float("nan")
