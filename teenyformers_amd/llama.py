@@ -389,8 +389,9 @@ class DecodeGraph:
     def _step(self):
         m = self.model
         h = m.hidden(self.ids, self.cache, self.pos)
-        nxt = ops.argmax_rows(m.logits(h[:, -1]))
-        self.ids.copy_(nxt.view(-1, 1))
+        # the greedy choice lands in the ids the next replay embeds (the
+        # embedding read them at the start of this step)
+        ops.argmax_rows(m.logits(h[:, -1]), out=self.ids.view(-1))
         self.pos.add_(1)
 
     def replay(self):
