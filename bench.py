@@ -334,9 +334,13 @@ def bench_bandwidth(torch, ops, lib, reps: int = 20):
 
 
 def bench_gemm(torch, reps: int = 20):
-    """The library's bf16 GEMM (teeny_linear_bf16, y = x W^T) at the prompt
-    shapes of the Llama-3-8B shape (16 x 512 tokens) and the Llama block
-    (4 x 2048 tokens), next to torch's GEMM (hipBLASLt) on the same operands."""
+    """bf16 y = x W^T at the prompt shapes of the Llama-3-8B shape (16 x 512
+    tokens) and the Llama block (4 x 2048 tokens): this library's own GEMM
+    kernel (teeny_gemm_bf16), its linear entry point (teeny_linear_bf16,
+    which hands these sizes to hipBLASLt) and torch's GEMM on the same
+    operands; for gate_up also the own GEMM with the SwiGLU epilogue
+    (teeny_linear_swiglu_bf16) against the linear entry point followed by the
+    SwiGLU kernel."""
     from teenyformers_amd import ops
 
     shapes = {"8b qkv": (8192, 6144, 4096), "8b o": (8192, 4096, 4096),
@@ -349,16 +353,33 @@ def bench_gemm(torch, reps: int = 20):
         w = (0.02 * torch.randn((N, K), device="cuda")).to(torch.bfloat16)
         y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
 
-        def lib_gemm():
+        def own_gemm():
+            ops.call("teeny_gemm_bf16", ops._p(x), ops._p(w), ops._p(y), M, N, K, ops._stream())
+
+        def lib_linear():
             ops.call("teeny_linear_bf16", ops._p(x), ops._p(w), ops._p(y), M, N, K, ops._stream())
 
-        ms = _time(torch, lib_gemm, reps)
+        ms = _time(torch, own_gemm, reps)
+        ms_l = _time(torch, lib_linear, reps)
         ms_t = _time(torch, lambda: torch.nn.functional.linear(x, w), reps)
         f = 2.0 * M * N * K
         res[name] = {"M": M, "N": N, "K": K, "ms": round(ms, 4),
                      "tflops": round(f / ms / 1e9, 1), "pct_peak": round(f / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+                     "linear_tflops": round(f / ms_l / 1e9, 1),
                      "hipblaslt_tflops": round(f / ms_t / 1e9, 1),
                      "vs_hipblaslt": round(ms_t / ms, 3)}
+        if "gate_up" in name:
+            F = N // 2
+            z = torch.empty((M, F), device="cuda", dtype=torch.bfloat16)
+
+            def fused():
+                ops.call("teeny_linear_swiglu_bf16", ops._p(x), ops._p(w), ops._p(z), M, F, K,
+                         ops._stream())
+
+            ms_f = _time(torch, fused, reps)
+            ms_u = _time(torch, lambda: ops.swiglu(ops.linear(x, w)), reps)
+            res[name].update({"swiglu_fused_ms": round(ms_f, 4), "linear_then_swiglu_ms": round(ms_u, 4)})
+            del z
         del x, w, y
     return res
 

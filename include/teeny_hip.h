@@ -304,10 +304,12 @@ int teeny_argmax_rows(const void* x, int64_t* out, int rows, int cols, int dtype
 /* Linear layer y[M, N] = x[M, K] . w[N, K]^T, bf16 only, any M >= 1: replaces
  * the external teeny-core Linear behind sym_linear (src/layers/mod.rs:54-58).
  * Up to 16 rows (a KV-cached decode step) with N % 128 == 0 and K % 128 == 0
- * stream the weight through a GEMV-shaped kernel; every other shape runs the
- * matrix-core GEMM, which requires N % 64 == 0 and K % 64 == 0 (otherwise
- * TEENY_ERR_UNSUPPORTED).  Either path is deterministic, with fp32
- * accumulation and one bf16 rounding of each output.
+ * stream the weight through a GEMV-shaped kernel; more rows go to hipBLASLt
+ * (faster than this library's GEMM at the Llama prompt shapes), and to
+ * teeny_gemm_bf16 where hipBLASLt does not take the device or shape; both
+ * require N % 64 == 0 and K % 64 == 0 (otherwise TEENY_ERR_UNSUPPORTED).
+ * Every path accumulates in fp32 and rounds each output to bf16 once; the
+ * hipBLASLt path keeps a workspace per (device, stream).
  * teeny_linear_swiglu_bf16: w is the fused gate_up weight [2F, K] (gate rows
  * first, src/loader.rs:49-55); writes y[M, F] = silu(x w_gate^T) *
  * (x w_up^T) with both products rounded to bf16 first, as FeedForward's
@@ -319,6 +321,11 @@ int teeny_argmax_rows(const void* x, int64_t* out, int rows, int cols, int dtype
  * followed by teeny_swiglu_fwd. */
 int teeny_linear_bf16(const void* x, const void* w, void* y, int M, int N, int K,
                       hipStream_t stream);
+/* This library's matrix-core GEMM for the same product, any M (N and K
+ * multiples of 64): teeny_linear_bf16's fallback above 16 rows, and the
+ * kernel whose epilogue forms teeny_linear_swiglu_bf16 at those sizes. */
+int teeny_gemm_bf16(const void* x, const void* w, void* y, int M, int N, int K,
+                    hipStream_t stream);
 int teeny_linear_swiglu_bf16(const void* x, const void* w, void* y, int M, int F, int K,
                              hipStream_t stream);
 

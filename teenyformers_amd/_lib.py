@@ -74,6 +74,7 @@ _SIGNATURES = {
                                        _i),
     "teeny_argmax_rows": ([_p, _p, _i, _i, _i, _p], _i),
     "teeny_linear_bf16": ([_p, _p, _p, _i, _i, _i, _p], _i),
+    "teeny_gemm_bf16": ([_p, _p, _p, _i, _i, _i, _p], _i),
     "teeny_linear_swiglu_bf16": ([_p, _p, _p, _i, _i, _i, _p], _i),
     "teeny_linear_partials_count": ([_i, _i], _i),
     "teeny_linear_partials_bf16": ([_p, _p, _p, _i, _i, _i, _i, _p], _i),

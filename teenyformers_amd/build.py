@@ -111,8 +111,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared",
         "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE}", f"-I{ROCM}/include",
         "-Wall", "-Wextra", "-Wno-unused-parameter",
-        os.path.join(CSRC, "capi.cpp"), blob_o, noalloc_o,
-        f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
+        os.path.join(CSRC, "capi.cpp"), os.path.join(CSRC, "blaslt.cpp"), blob_o, noalloc_o,
+        f"-L{ROCM}/lib", "-lhipblaslt", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
         "-o", tmp,
     ]
     _run(cmd, verbose)

@@ -40,6 +40,9 @@
 
 // noalloc.hip: the current device's address of its static scratch array
 extern "C" __attribute__((visibility("hidden"))) int teeny_scratch_setup(void** out);
+// blaslt.cpp: a prompt-size product through hipBLASLt (0), or -1 to fall back
+extern "C" __attribute__((visibility("hidden"))) int teeny_lt_gemm_bf16(
+    const void* x, const void* w, void* y, int M, int N, int K, hipStream_t stream);
 
 #define TEENY_CO_DECL(n) \
   extern "C" const unsigned char teeny_co_##n[]; \
@@ -960,9 +963,25 @@ static int linear_sk_check(const void* x, const void* w, const void* y, int M, i
   return TEENY_OK;
 }
 
+// This library's matrix-core GEMM (gemm_bf16.hip: 256 x 256 tiles of y, 512
+// threads), any M; N and K multiples of 64.
+int teeny_gemm_bf16(const void* x, const void* w, void* y, int M, int N, int K,
+                    hipStream_t stream) {
+  if (!x || !w || !y) return TEENY_ERR_NULL_POINTER;
+  if (M <= 0 || N <= 0 || K <= 0 || (long)N * K >= kMaxElems * 2) return TEENY_ERR_INVALID_SHAPE;
+  if (N % 64 != 0 || K % 64 != 0) return TEENY_ERR_UNSUPPORTED;
+  // a workgroup addresses its 256 rows of x and of w with 32-bit byte offsets
+  if ((long)K * 2 * 256 >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
+  int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
+  if ((long)tiles_m * tiles_n >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
+  void* args[] = {&x, &w, &y, &M, &N, &K, &tiles_m, &tiles_n};
+  return launch("teeny_gemm_bf16_nt", dim3(tiles_m * tiles_n), dim3(512), 0, stream, args);
+}
+
 // Any M: up to 16 rows (a decode step) stream the weight through
-// linear_bf16.hip's kernels when N and K are multiples of 128; otherwise the
-// matrix-core GEMM (gemm_bf16.hip: 256 x 256 tiles of y, 512 threads).
+// linear_bf16.hip's kernels when N and K are multiples of 128; more rows go
+// to hipBLASLt (blaslt.cpp), or to teeny_gemm_bf16 where hipBLASLt is not
+// available for the device or shape.
 int teeny_linear_bf16(const void* x, const void* w, void* y, int M, int N, int K,
                       hipStream_t stream) {
   if (!x || !w || !y) return TEENY_ERR_NULL_POINTER;
@@ -972,12 +991,9 @@ int teeny_linear_bf16(const void* x, const void* w, void* y, int M, int N, int K
     return launch("teeny_linear_sk_bf16", dim3(N / 128), dim3(512), 0, stream, args);
   }
   if (N % 64 != 0 || K % 64 != 0) return TEENY_ERR_UNSUPPORTED;
-  // a workgroup addresses its 256 rows of x and of w with 32-bit byte offsets
   if ((long)K * 2 * 256 >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
-  int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
-  if ((long)tiles_m * tiles_n >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
-  void* args[] = {&x, &w, &y, &M, &N, &K, &tiles_m, &tiles_n};
-  return launch("teeny_gemm_bf16_nt", dim3(tiles_m * tiles_n), dim3(512), 0, stream, args);
+  if (M > 16 && teeny_lt_gemm_bf16(x, w, y, M, N, K, stream) == 0) return TEENY_OK;
+  return teeny_gemm_bf16(x, w, y, M, N, K, stream);
 }
 
 // Any M, as teeny_linear_bf16: up to 16 rows through linear_bf16.hip's

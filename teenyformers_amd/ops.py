@@ -507,17 +507,32 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return y.view(*x.shape[:-1], N)
 
 
+def gemm_own(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x w^T through this library's own matrix-core GEMM (teeny_gemm_bf16),
+    any row count, bf16, no gradients (teeny_linear_bf16 hands prompt sizes
+    to hipBLASLt instead)."""
+    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    N, K = w.shape
+    if K != x2.shape[1] or not _gemm(x2, w):
+        raise ValueError("gemm_own: bf16 x [.., K] and contiguous w [N, K], N and K multiples of 64")
+    y = torch.empty((x2.shape[0], N), dtype=x.dtype, device=x.device)
+    call("teeny_gemm_bf16", _p(x2), _p(w), _p(y), x2.shape[0], N, K, _stream())
+    return y.view(*x.shape[:-1], N)
+
+
 def linear_swiglu(x: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
-    """swiglu(x w_gate_up^T) (src/layers/ffn.rs:47-56) in one launch of
-    teeny_linear_swiglu_bf16 for bf16 without gradients (the weight-streaming
-    kernel up to 16 rows, the GEMM with a SwiGLU epilogue above), bit-identical
-    to the GEMM followed by the SwiGLU kernel, which other cases run."""
+    """swiglu(x w_gate_up^T) (src/layers/ffn.rs:47-56).  Up to 16 bf16 rows
+    without gradients: one launch of teeny_linear_swiglu_bf16 (the decode
+    kernel with the SwiGLU fused).  More rows: the linear entry point
+    (hipBLASLt) and then the SwiGLU kernel, measured faster than the own GEMM
+    with the SwiGLU epilogue (1.40 against 1.52 ms at 8192 x 28672 x 4096);
+    other cases: the GEMM followed by the SwiGLU kernel."""
     x2 = x.reshape(-1, x.shape[-1])
     N2, K = w_gate_up.shape
     if K != x2.shape[1] or N2 % 2:
         raise ValueError("linear_swiglu: weight must be [2F, in] with in = x's features")
     F = N2 // 2
-    if not _gemm(x2, w_gate_up):
+    if not _gemm(x2, w_gate_up) or not _skinny(x2, w_gate_up, F, row_tile=64):
         return swiglu(linear(x, w_gate_up))
     x2 = x2.contiguous()
     y = torch.empty((x2.shape[0], F), dtype=x.dtype, device=x.device)
