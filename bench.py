@@ -359,9 +359,11 @@ def bench_gemm(torch, reps: int = 20):
         def lib_linear():
             ops.call("teeny_linear_bf16", ops._p(x), ops._p(w), ops._p(y), M, N, K, ops._stream())
 
-        ms = _time(torch, own_gemm, reps)
-        ms_l = _time(torch, lib_linear, reps)
-        ms_t = _time(torch, lambda: torch.nn.functional.linear(x, w), reps)
+        # several warm-up calls: a library's first call of a shape also
+        # creates its plan and loads its kernel, longer than the warm-up time
+        ms = _time(torch, own_gemm, reps, warmup=5)
+        ms_l = _time(torch, lib_linear, reps, warmup=5)
+        ms_t = _time(torch, lambda: torch.nn.functional.linear(x, w), reps, warmup=5)
         f = 2.0 * M * N * K
         res[name] = {"M": M, "N": N, "K": K, "ms": round(ms, 4),
                      "tflops": round(f / ms / 1e9, 1), "pct_peak": round(f / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
@@ -376,8 +378,8 @@ def bench_gemm(torch, reps: int = 20):
                 ops.call("teeny_linear_swiglu_bf16", ops._p(x), ops._p(w), ops._p(z), M, F, K,
                          ops._stream())
 
-            ms_f = _time(torch, fused, reps)
-            ms_u = _time(torch, lambda: ops.swiglu(ops.linear(x, w)), reps)
+            ms_f = _time(torch, fused, reps, warmup=5)
+            ms_u = _time(torch, lambda: ops.swiglu(ops.linear(x, w)), reps, warmup=5)
             res[name].update({"swiglu_fused_ms": round(ms_f, 4), "linear_then_swiglu_ms": round(ms_u, 4)})
             del z
         del x, w, y
