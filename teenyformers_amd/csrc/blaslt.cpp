@@ -13,7 +13,8 @@
 // the activations' memory as a K x M column-major matrix, D y's memory as an
 // N x M column-major matrix.  Plans (descriptors and the heuristic's first
 // algorithm) are cached per (device, M, N, K); each (device, stream) gets
-// its own workspace, so products on different streams never share one.
+// its own workspace, so products on different streams never share one.  The
+// handle, plans and workspaces live until the process ends.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -79,22 +80,32 @@ extern "C" __attribute__((visibility("hidden"))) int teeny_lt_gemm_bf16(
     const void* x, const void* w, void* y, int M, int N, int K, hipStream_t stream) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return -1;
+  // under stream capture nothing is created (handle, plan, workspace): a
+  // shape met first inside a capture runs the caller's own GEMM
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return -1;
+  const bool capturing = cap != hipStreamCaptureStatusNone;
   std::lock_guard<std::mutex> lock(mu);
   Device& d = devices[dev];
   if (!d.tried) {
+    if (capturing) return -1;
     d.tried = true;
     if (hipblasLtCreate(&d.handle) != HIPBLAS_STATUS_SUCCESS) d.handle = nullptr;
   }
   if (!d.handle) return -1;
   auto key = std::make_tuple(M, N, K);
   auto it = d.plans.find(key);
-  if (it == d.plans.end()) it = d.plans.emplace(key, make_plan(d.handle, M, N, K)).first;
+  if (it == d.plans.end()) {
+    if (capturing) return -1;
+    it = d.plans.emplace(key, make_plan(d.handle, M, N, K)).first;
+  }
   const Plan& p = it->second;
   if (!p.ok) return -1;
   // the whole workspace goes with every call (the heuristic chose its
   // algorithm under that limit)
   auto wi = d.workspace.find(stream);
   if (wi == d.workspace.end()) {
+    if (capturing) return -1;
     void* buf = nullptr;
     if (hipMalloc(&buf, kWorkspace) != hipSuccess) return -1;
     wi = d.workspace.emplace(stream, buf).first;

@@ -83,3 +83,27 @@ def test_gemm_linear_op(cuda):
     assert torch.equal(ops.gemm_own(_dev(x), _dev(w)), _gemm(_dev(x), _dev(w), "teeny_gemm_bf16"))
     xs = _dev(x[:16])
     assert torch.equal(ops.linear(xs, _dev(w)), _gemm(xs, _dev(w)))
+
+
+def test_linear_under_graph_capture(cuda):
+    """A prompt-size teeny_linear_bf16 first met inside a HIP graph capture
+    runs the own GEMM (hipBLASLt's handle, plan and workspace are created
+    outside captures only); the graph replays give the eager bits each
+    time, with eager work between the replays."""
+    M, N, K = 320, 384, 512
+    x, w = _operands(M, N, K, seed=9)
+    xd, wd = _dev(x), _dev(w)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        _lib.call("teeny_linear_bf16", ops._p(xd), ops._p(wd), ops._p(y), M, N, K,
+                  torch.cuda.current_stream().cuda_stream)
+    own = _gemm(xd, wd, "teeny_gemm_bf16")
+    for _ in range(3):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, own)
+        _check(_gemm(xd, wd).float().cpu().numpy(), x, w)  # eager: hipBLASLt
