@@ -61,7 +61,7 @@ struct __attribute__((aligned(16))) FwdSmem {
 };
 
 // NW wavefronts (4 or 8) of 32 query rows each
-template <int D, bool CAUSAL, int NW = 4>
+template <int D, bool CAUSAL, int NW = 4, bool PACK = false>
 __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict__ k,
                              const bf16* __restrict__ v, bf16* __restrict__ o,
                              float* __restrict__ lse, int nq, int nk, float scale, int hq, int hkv,
@@ -85,11 +85,28 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   int bh, rank;
   pair_order(id, num_m_blocks, total_blocks / num_m_blocks, bh, rank);
   const int mb = num_m_blocks - 1 - rank;  // the last query block is the heaviest
-  const int b = bh / hq, h = bh - b * hq;
-  const long kvh = (long)b * hkv + h / (hq / hkv);
-  const int m0 = mb * BM;
-  const int qrow = m0 + wave * 32 + l32;
-  const int wave_qmax = m0 + wave * 32 + 31;
+  // bhq: this wavefront's (b, q head); wrow0: its first query row; blk_end:
+  // one past the workgroup's last row.  GQA-packed (PACK, NW = hq / hkv): bh
+  // is a (b, kv head), every wavefront takes the same 32 rows of its own q
+  // head of the group; otherwise bh is a (b, q head) and wavefront w takes
+  // rows 32 w of the block's BM.
+  int bhq, wrow0, blk_end;
+  long kvh;
+  if constexpr (PACK) {
+    const int b = bh / hkv;
+    kvh = bh;
+    bhq = b * hq + (bh - b * hkv) * NW + wave;
+    wrow0 = mb * 32;
+    blk_end = wrow0 + 32;
+  } else {
+    const int b = bh / hq, h = bh - b * hq;
+    kvh = (long)b * hkv + h / (hq / hkv);
+    bhq = bh;
+    wrow0 = mb * BM + wave * 32;
+    blk_end = mb * BM + BM;
+  }
+  const int qrow = wrow0 + l32;
+  const int wave_qmax = wrow0 + 31;
 
   const bf16* kb = k + kvh * (long)nk * D;
   const bf16* vb = v + kvh * (long)nk * D;
@@ -98,13 +115,13 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   // rows past nq load row nq - 1: computed, never stored
   bf16x8 qreg[DC];
   {
-    const bf16* qp = q + ((long)bh * nq + min(qrow, nq - 1)) * D + 8 * g;
+    const bf16* qp = q + ((long)bhq * nq + min(qrow, nq - 1)) * D + 8 * g;
 #pragma unroll
     for (int c = 0; c < DC; ++c) qreg[c] = as_bf16x8(*reinterpret_cast<const u32x4*>(qp + 16 * c));
   }
 
   int kend = nk;
-  if (CAUSAL) kend = min(nk, m0 + BM);
+  if (CAUSAL) kend = min(nk, blk_end);
   const int n_iter = (kend + BN - 1) / BN;
   // causal: the workgroup's tiles past this wavefront's last row are fully
   // masked for it; it computes only the first n_live (wave-uniform)
@@ -225,7 +242,7 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   // raw scores of keys past the sequence or (causal) past the row -> -inf;
   // only tiles that reach past nk or past the wave's first row need it
   auto mask = [&](int kbase, f32x16& s0, f32x16& s1) {
-    if ((kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > m0 + wave * 32)) {
+    if ((kbase + BN > nk) || (CAUSAL && kbase + BN - 1 > wrow0)) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         int key = kbase + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -426,7 +443,7 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   const float l_tot = l_run + other_half(l_run);
   if (qrow < nq) {
     const float inv = 1.0f / l_tot;
-    bf16* orow = o + ((long)bh * nq + qrow) * D;
+    bf16* orow = o + ((long)bhq * nq + qrow) * D;
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
 #pragma unroll
@@ -437,7 +454,7 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
         *reinterpret_cast<u32x2*>(orow + d) = w;
       }
     }
-    if (g == 0) lse[(long)bh * nq + qrow] = (m_run + __log2f(l_tot)) * kLn2;
+    if (g == 0) lse[(long)bhq * nq + qrow] = (m_run + __log2f(l_tot)) * kLn2;
   }
 }
 
@@ -470,3 +487,28 @@ TEENY_FA2_FWD_BF16_INST(128)
   }
 TEENY_FA2_FWD_BF16_W8_INST(128, true, c)
 TEENY_FA2_FWD_BF16_W8_INST(128, false, n)
+
+// GQA-packed: one workgroup per (b, kv head, 32 query rows), wavefront w on
+// q head kv head * 4 + w (hq = 4 hkv); every wavefront of a causal block
+// ends on the same row, so none waits out the block's last tiles
+#define TEENY_FA2_FWD_BF16_G4_INST(D, C, CZ)                                                    \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
+  void teeny_fa2_fwd_bf16_d##D##_##CZ##_g4(                                                      \
+      const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,            \
+      float scale, int hq, int hkv, int nmb, int total) {                                        \
+    fa2_fwd_bf16<D, C, 4, true>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);              \
+  }
+
+TEENY_FA2_FWD_BF16_G4_INST(64, true, c)
+TEENY_FA2_FWD_BF16_G4_INST(128, true, c)
+
+// 8 wavefronts: q heads kv head * 8 + w (hq = 8 hkv)
+#define TEENY_FA2_FWD_BF16_G8_INST(D, C, CZ)                                                    \
+  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
+  void teeny_fa2_fwd_bf16_d##D##_##CZ##_g8(                                                      \
+      const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,            \
+      float scale, int hq, int hkv, int nmb, int total) {                                        \
+    fa2_fwd_bf16<D, C, 8, true>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);              \
+  }
+
+TEENY_FA2_FWD_BF16_G8_INST(128, true, c)

@@ -140,6 +140,9 @@ BF16_SHAPES = [  # B, Hq, Hkv, Sq, Sk, D
     (1, 4, 2, 300, 100, 64),    # Sq > Sk
     (1, 2, 2, 1, 1, 64),        # one row
     (1, 2, 2, 1024, 1024, 128),
+    (2, 8, 2, 200, 260, 64),    # causal: GQA 4 packed (a wavefront per q head), Sq < Sk
+    (1, 8, 2, 300, 100, 64),    # GQA 4 packed, Sq > Sk
+    (1, 16, 2, 333, 333, 128),  # GQA 8 packed
 ]
 
 
