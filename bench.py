@@ -62,7 +62,7 @@ def main() -> int:
                     help="skip the long-context GQA, Llama block and Llama-8B measurements")
     ap.add_argument("--no-power", action="store_true",
                     help="skip the power / clock sampling phase")
-    ap.add_argument("--only", choices=["bandwidth", "block", "gqa", "llama8b", "gemm"],
+    ap.add_argument("--only", choices=["bandwidth", "block", "gqa", "gqa_short", "llama8b", "gemm"],
                     help="run only one of the secondary measurements (one JSON line): the "
                          "HBM-bound kernels at the Llama-block shapes, one Llama block, the "
                          "long-context GQA FA2, or the Llama-8B-shape prefill + decode")
@@ -87,6 +87,7 @@ def main() -> int:
         run = {"bandwidth": ("bandwidth_c2", lambda: bench_bandwidth(torch, ops, _lib)),
                "block": ("llama_block", lambda: bench_llama_block(torch)),
                "gqa": ("fa2_gqa_long", lambda: bench_gqa_long(torch, ops)),
+               "gqa_short": ("fa2_gqa_short", lambda: bench_gqa_short(torch, ops)),
                "llama8b": ("llama_8b_shape", lambda: bench_llama_8b(torch)),
                "gemm": ("gemm", lambda: bench_gemm(torch))}[args.only]
         print(json.dumps({run[0]: run[1]()}), flush=True)
@@ -188,6 +189,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         out["detail"]["bandwidth_c2"] = bench_bandwidth(torch, ops, _lib)
         out["detail"]["fa2_gqa_long"] = bench_gqa_long(torch, ops)
+        out["detail"]["fa2_gqa_short"] = bench_gqa_short(torch, ops)
         out["detail"]["gemm"] = bench_gemm(torch)
         out["detail"]["llama_block"] = bench_llama_block(torch)
         out["detail"]["llama_8b_shape"] = bench_llama_8b(torch)
@@ -246,6 +248,28 @@ def bench_gqa_long(torch, ops):
                          "bwd_pct_peak": round(2.5 * f / bwd_ms / 1e9 / PEAK_BF16_TFLOPS, 4)}
         del q, k, v, do, o, lse
     return res
+
+
+def bench_gqa_short(torch, ops):
+    """Causal GQA FA2 at the Llama-3-8B prefill's attention shape, B16 Hq32
+    Hkv8 S512 D128: forward (the prompt path) and backward, events around 20
+    calls."""
+    B_, Hq, Hkv, S_, D_ = 16, 32, 8, 512, 128
+    gen = torch.Generator(device="cuda").manual_seed(512)
+    q = torch.randn((B_, Hq, S_, D_), generator=gen, device="cuda").to(torch.bfloat16)
+    k = torch.randn((B_, Hkv, S_, D_), generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn((B_, Hkv, S_, D_), generator=gen, device="cuda").to(torch.bfloat16)
+    do = torch.randn_like(q)
+    sc = 1.0 / math.sqrt(D_)
+    o, lse = ops.flash_attn2_fwd(q, k, v, sc, True)
+    fwd_ms = _time(torch, lambda: ops.flash_attn2_fwd(q, k, v, sc, True, out=o, lse=lse), 20)
+    bwd_ms = _time(torch, lambda: ops.flash_attn2_bwd(q, k, v, o, lse, do, sc, True), 20)
+    f = fwd_flops(B_, Hq, S_, S_, D_)
+    return {"shape": f"B{B_} Hq{Hq} Hkv{Hkv} S{S_} D{D_} causal",
+            "fwd_us": round(fwd_ms * 1e3, 1), "bwd_us": round(bwd_ms * 1e3, 1),
+            "fwd_tflops": round(f / fwd_ms / 1e9, 1), "bwd_tflops": round(2.5 * f / bwd_ms / 1e9, 1),
+            "fwd_pct_peak": round(f / fwd_ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+            "bwd_pct_peak": round(2.5 * f / bwd_ms / 1e9 / PEAK_BF16_TFLOPS, 4)}
 
 
 def bench_bandwidth(torch, ops, lib, reps: int = 20):

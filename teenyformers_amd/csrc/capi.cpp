@@ -338,13 +338,17 @@ int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void
   char name[64];
   if (dtype == TEENY_BF16) {
     float* ld = (float*)workspace;
-    // dQ first: one workgroup per 128 query rows of a (b, q head); it also
-    // writes LSE * log2(e) and Delta of its rows to ld for the dK/dV kernel
-    int nmb = (n_ctx_q + 127) / 128;
-    long total = (long)nmb * batch * hq;
+    // dQ first: one workgroup per 128 query rows of a (b, q head), or, for
+    // causal GQA groups of 4, per (b, kv head, 32 rows) with a wavefront per
+    // q head as in the forward; it also writes LSE * log2(e) and Delta of
+    // its rows to ld for the dK/dV kernel
+    const bool pack = causal && hq == 4 * hkv;
+    int nmb = pack ? (n_ctx_q + 31) / 32 : (n_ctx_q + 127) / 128;
+    long total = (long)nmb * batch * (pack ? hkv : hq);
     if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
     int tot = (int)total;
-    snprintf(name, sizeof name, "teeny_fa2_bwd_dq_bf16_d%d_%s%s", head_dim, cz, gsfx);
+    snprintf(name, sizeof name, "teeny_fa2_bwd_dq_bf16_d%d_%s%s%s", head_dim, cz,
+             pack ? "_g4" : "", gsfx);
     void* a2[] = {&q,       &k,       &v,     &o,  &dout, &l,   &ld,  &dq,
                   &n_ctx_q, &n_ctx_k, &scale, &hq, &hkv,  &nmb, &tot};
     rc = launch(name, dim3(tot), dim3(256), 0, stream, a2);

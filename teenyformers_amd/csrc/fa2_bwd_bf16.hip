@@ -413,7 +413,9 @@ struct __attribute__((aligned(16))) DqSmem {
   char v[QVBUF][QBN * D * 2];
 };
 
-template <int D, bool CAUSAL, typename GT>
+// PACK: GQA groups of 4 packed as in the forward, one workgroup per (b, kv
+// head, 32 query rows), wavefront w on q head kv head * 4 + w
+template <int D, bool CAUSAL, typename GT, bool PACK = false>
 __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ k,
                            const bf16* __restrict__ v, const bf16* __restrict__ o,
                            const bf16* __restrict__ dout, const float* __restrict__ lse,
@@ -439,10 +441,24 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   int bh, rank;
   pair_order(id, num_m_blocks, total_blocks / num_m_blocks, bh, rank);
   const int mb = num_m_blocks - 1 - rank;  // the last query block is the heaviest
-  const int b = bh / hq, h = bh - b * hq;
-  const long kvh = (long)b * hkv + h / (hq / hkv);
-  const int m0 = mb * QBM;
-  const int qrow = m0 + wave * 32 + l32;
+  // bhq: this wavefront's (b, q head); wrow0: its first query row; blk_end:
+  // one past the workgroup's last row
+  int bhq, wrow0, blk_end;
+  long kvh;
+  if constexpr (PACK) {
+    const int b = bh / hkv;
+    kvh = bh;
+    bhq = b * hq + (bh - b * hkv) * 4 + wave;
+    wrow0 = mb * 32;
+    blk_end = wrow0 + 32;
+  } else {
+    const int b = bh / hq, h = bh - b * hq;
+    kvh = (long)b * hkv + h / (hq / hkv);
+    bhq = bh;
+    wrow0 = mb * QBM + wave * 32;
+    blk_end = mb * QBM + QBM;
+  }
+  const int qrow = wrow0 + l32;
   const bool qok = qrow < nq;
 
   const bf16* kb = k + kvh * (long)nk * D;
@@ -452,7 +468,7 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   // rows past nq load row nq - 1 and get LSE = +inf (P = 0): never stored
   bf16x8 qreg[DC], doreg[DC];
   {
-    const long row = (long)bh * nq + min(qrow, nq - 1);
+    const long row = (long)bhq * nq + min(qrow, nq - 1);
     const bf16* qp = q + row * D + 8 * g;
     const bf16* dp = dout + row * D + 8 * g;
 #pragma unroll
@@ -467,7 +483,7 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   // runs after this one.
   float lse2 = INFINITY, dlt = 0.0f;
   {
-    const long row = (long)bh * nq + min(qrow, nq - 1);
+    const long row = (long)bhq * nq + min(qrow, nq - 1);
     const bf16* op = o + row * D + 8 * g;
     float part = 0.0f;
 #pragma unroll
@@ -485,12 +501,12 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
     }
     part += other_half(part);
     if (qok) {
-      lse2 = lse[(long)bh * nq + qrow] * kLog2e;
+      lse2 = lse[(long)bhq * nq + qrow] * kLog2e;
       dlt = part;
     }
     const int nq_pad = (nq + BM - 1) / BM * BM;  // ld rows: whole blocks of BM
     if (g == 0 && qrow < nq_pad) {
-      float* blk = ld + ((long)bh * nq_pad + qrow) / BM * (2 * BM);
+      float* blk = ld + ((long)bhq * nq_pad + qrow) / BM * (2 * BM);
       blk[qrow % BM] = lse2;
       blk[BM + qrow % BM] = dlt;
     }
@@ -498,11 +514,11 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   const float sl2 = scale * kLog2e;
 
   int kend = nk;
-  if (CAUSAL) kend = min(nk, m0 + QBM);
+  if (CAUSAL) kend = min(nk, blk_end);
   const int n_iter = (kend + QBN - 1) / QBN;
   // causal: the workgroup's tiles past this wavefront's last row are fully
   // masked for it; it computes only the first n_live (wave-uniform)
-  const int n_live = CAUSAL ? min(n_iter, (m0 + wave * 32 + 31) / QBN + 1) : n_iter;
+  const int n_live = CAUSAL ? min(n_iter, (wrow0 + 31) / QBN + 1) : n_iter;
 
   // ---- K / V tiles: buffer_load ... lds, both SWZ_DUAL ----------------------
   const uint32_t src = swz<SWZ_DUAL, D>(wave * 64 + lane) * 16;
@@ -592,7 +608,7 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   };
   // keys past nk or (causal) past the row -> score -inf, so P = dS = 0
   auto mask = [&](int kb0, f32x16& s) {
-    if ((kb0 + 32 > nk) || (CAUSAL && kb0 + 31 > m0 + wave * 32)) {
+    if ((kb0 + 32 > nk) || (CAUSAL && kb0 + 31 > wrow0)) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kb0 + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -725,7 +741,7 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   }
 
   if (qok) {
-    GT* dqr = dq + ((long)bh * nq + qrow) * D;
+    GT* dqr = dq + ((long)bhq * nq + qrow) * D;
 #pragma unroll
     for (int t = 0; t < DT; ++t)
 #pragma unroll
@@ -768,6 +784,22 @@ TEENY_FA2_BWD_BF16_INST(64, c, true, float, _g32)
 TEENY_FA2_BWD_BF16_INST(64, n, false, float, _g32)
 TEENY_FA2_BWD_BF16_INST(128, c, true, float, _g32)
 TEENY_FA2_BWD_BF16_INST(128, n, false, float, _g32)
+
+// dQ of causal GQA groups of 4, packed (hq = 4 hkv)
+#define TEENY_FA2_BWD_DQ_G4_INST(D, GT, SFX)                                                     \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
+  void teeny_fa2_bwd_dq_bf16_d##D##_c_g4##SFX(                                                  \
+      const bf16* q, const bf16* k, const bf16* v, const bf16* o, const bf16* dout,             \
+      const float* lse, float* ld, GT* dq, int nq, int nk, float scale, int hq, int hkv,        \
+      int nmb, int total) {                                                                     \
+    fa2_bwd_dq<D, true, GT, true>(q, k, v, o, dout, lse, ld, dq, nq, nk, scale, hq, hkv, nmb,  \
+                                  total);                                                       \
+  }
+
+TEENY_FA2_BWD_DQ_G4_INST(64, bf16, )
+TEENY_FA2_BWD_DQ_G4_INST(128, bf16, )
+TEENY_FA2_BWD_DQ_G4_INST(64, float, _g32)
+TEENY_FA2_BWD_DQ_G4_INST(128, float, _g32)
 
 extern "C" __global__ __launch_bounds__(256) void teeny_fa2_dkdv_merge_bf16(
     const float* part, bf16* dk, bf16* dv, long n, int hsplit, float scale) {
