@@ -96,7 +96,7 @@ def test_noalloc_bwd_refuses_beyond_scratch(L):
 
 def test_fa2_bwd_workspace_gqa(L):
     """The larger workspace that allows the dK/dV head split: only for bf16
-    GQA with few key blocks (here 64 blocks x 8 kv heads = 512 workgroups,
+    GQA with 1024+ query rows and few key blocks (here 64 blocks x 8 kv heads = 512 workgroups,
     two per CU of a 256-CU device without a GPU to ask), fp32 dK and dV
     partials for 2 splits on top of the base workspace."""
     f = L.teeny_flash_attn2_bwd_workspace_bytes_gqa
@@ -107,6 +107,11 @@ def test_fa2_bwd_workspace_gqa(L):
         4096, 8, 32, 128, BF16)
     assert f(16384, 16384, 1, 64, 8, 128, BF16) == L.teeny_flash_attn2_bwd_workspace_bytes(
         16384, 1, 64, 128, BF16)
+    # fewer than 1024 query rows: short walks, no split (B16 Hq32 Hkv8 S512)
+    assert f(512, 512, 16, 32, 8, 128, BF16) == L.teeny_flash_attn2_bwd_workspace_bytes(
+        512, 16, 32, 128, BF16)
+    assert f(1024, 1024, 4, 32, 8, 128, BF16) > L.teeny_flash_attn2_bwd_workspace_bytes(
+        1024, 4, 32, 128, BF16)
     assert f(128, 128, 1, 4, 2, 64, F32) == L.teeny_flash_attn2_bwd_workspace_bytes(
         128, 1, 4, 64, F32)
     assert f(128, 128, 1, 6, 4, 64, BF16) == 0  # Hq % Hkv != 0
