@@ -384,15 +384,27 @@ __device__ void argmax_rows(const T* __restrict__ x, long long* __restrict__ out
   };
   constexpr int VN = Vec16<T>::N;
   if (cols % VN == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
-    for (int c = threadIdx.x * VN; c < cols; c += kArgThreads * VN) {
-      float a[VN];
-      Vec16<T>::load(row + c, a);
+    // U vectors (64 values) per thread requested before the first
+    // comparison (one at a time, the row took ~16 dependent memory round
+    // trips); `better` is a strict total order, so the visiting order does
+    // not change the result
+    constexpr int U = 64 / VN, STEP = kArgThreads * VN;
+    for (int c0 = threadIdx.x * VN; c0 < cols; c0 += U * STEP) {
+      float a[U][VN];
 #pragma unroll
-      for (int j = 0; j < VN; ++j)
-        if (better(a[j], c + j, v, idx)) {
-          v = a[j];
-          idx = c + j;
-        }
+      for (int u = 0; u < U; ++u)
+        if (c0 + u * STEP < cols) Vec16<T>::load(row + c0 + u * STEP, a[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * STEP;
+        if (c < cols)
+#pragma unroll
+          for (int j = 0; j < VN; ++j)
+            if (better(a[u][j], c + j, v, idx)) {
+              v = a[u][j];
+              idx = c + j;
+            }
+      }
     }
   } else {
     for (int c = threadIdx.x; c < cols; c += kArgThreads) {

@@ -204,11 +204,13 @@ def test_argmax_rows(cuda, dtype):
     x[5, :] = 0.0                # all equal: the last index
     x[9, 123] = float("nan")     # NaN is the maximum
     x[11, :] = float("-inf")     # all -inf: the last index
+    x[13, 5] = x[13, 70000] = float("nan")  # two NaNs, in different load batches: the last
     got = ops.argmax_rows(x)
     n = x.shape[1]
     # torch.argmax keeps the first maximum (and the first NaN): flip the row
     assert torch.equal(got, n - 1 - torch.argmax(x.flip(-1), dim=-1))
     assert got[3] == 90000 and got[5] == n - 1 and got[9] == 123 and got[11] == n - 1
+    assert got[13] == 70000
     # a row whose length is not a multiple of the vector width
     y = x[:, :1001].contiguous()
     assert torch.equal(ops.argmax_rows(y), 1000 - torch.argmax(y.flip(-1), dim=-1))
