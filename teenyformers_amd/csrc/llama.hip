@@ -385,10 +385,13 @@ __device__ void argmax_rows(const T* __restrict__ x, long long* __restrict__ out
   constexpr int VN = Vec16<T>::N;
   if (cols % VN == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
     // U vectors (64 values) per thread requested before the first
-    // comparison (one at a time, the row took ~16 dependent memory round
-    // trips); `better` is a strict total order, so the visiting order does
-    // not change the result
+    // comparison.  A thread meets its indices in increasing order, so
+    // `x >= v` keeps the last of equal maxima (-0 and +0 compare equal, as
+    // in the reference) and NaN, which compares false, is tracked apart;
+    // branch-free, one compare and two selects per value (the comparison
+    // through `better` made every value a divergent branch, ~20 µs a row)
     constexpr int U = 64 / VN, STEP = kArgThreads * VN;
+    int nan_idx = -1;
     for (int c0 = threadIdx.x * VN; c0 < cols; c0 += U * STEP) {
       float a[U][VN];
 #pragma unroll
@@ -399,12 +402,18 @@ __device__ void argmax_rows(const T* __restrict__ x, long long* __restrict__ out
         const int c = c0 + u * STEP;
         if (c < cols)
 #pragma unroll
-          for (int j = 0; j < VN; ++j)
-            if (better(a[u][j], c + j, v, idx)) {
-              v = a[u][j];
-              idx = c + j;
-            }
+          for (int j = 0; j < VN; ++j) {
+            const float x = a[u][j];
+            const bool ge = x >= v;
+            v = ge ? x : v;
+            idx = ge ? c + j : idx;
+            nan_idx = x != x ? c + j : nan_idx;
+          }
       }
+    }
+    if (nan_idx >= 0) {  // NaN is the maximum: the thread's last NaN
+      v = __builtin_nanf("");
+      idx = nan_idx;
     }
   } else {
     for (int c = threadIdx.x; c < cols; c += kArgThreads) {
