@@ -214,8 +214,9 @@ struct __attribute__((aligned(16))) DecQkvSmem {
       float o[kDqWaves][32 * D];
     } c;
   } u;
-  bf16 q[32 * D];  // the group's RoPE'd q rows
-  bf16 kv[2][D];   // the new cache row: k (RoPE'd), v
+  bf16 q[32 * D];      // the group's RoPE'd q rows
+  bf16 kv[2][D];       // the new cache row: k (RoPE'd), v
+  float cs[D / 2][2];  // (cos, sin) of the pair angles at the new position
 };
 
 template <int D>
@@ -268,30 +269,58 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
   if (n_tiles > 0) load(k0);
 
   // ---- 1. q, k, v of position pos -------------------------------------------
-  const float c = (-2.0f * ln_base) / (float)D;
-  for (int i = tid; i < (group + 2) * (D / VN); i += kDqWaves * 64) {
-    const int hh = i / (D / VN), vv = i - hh * (D / VN);
-    const int row = hh < group ? hk * group + hh : (hh == group ? hq + hk : hq + hkv + hk);
-    float in[VN];
-    ld_parts<bf16, VN>(parts + ((long)b * htot + row) * D + vv * VN, part_stride, n_parts, in);
-    float out[VN];
-    if (hh <= group) {  // q and k: RoPE on the interleaved pairs
+  // A thread sums the K-split slabs of up to two 16-byte items (group + 2
+  // rows of D / VN items; group <= 32).  The (cos, sin) of the D / 2 pair
+  // angles at position pos are the same for every q head and k: the last
+  // D / 2 threads evaluate them once, into LDS, while the slab loads fly
+  // (evaluated per item they were 4 serial exp / sincos chains per thread).
+  constexpr int NT = kDqWaves * 64;
+  const int n_items = (group + 2) * (D / VN);
+  float in[2][VN];
 #pragma unroll
-      for (int j = 0; j < VN / 2; ++j) {
-        const int kk = vv * (VN / 2) + j;
-        const float inv = (float)exp((double)((float)kk * c));
-        const float theta = (float)pos * inv;
-        float sn, cn;
-        sincosf(theta, &sn, &cn);
-        out[2 * j] = in[2 * j] * cn - in[2 * j + 1] * sn;
-        out[2 * j + 1] = in[2 * j] * sn + in[2 * j + 1] * cn;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < VN; ++j) out[j] = in[j];
+  for (int r = 0; r < 2; ++r) {
+    const int i = tid + r * NT;
+    if (i < n_items) {
+      const int hh = i / (D / VN), vv = i - hh * (D / VN);
+      const int row = hh < group ? hk * group + hh : (hh == group ? hq + hk : hq + hkv + hk);
+      ld_parts<bf16, VN>(parts + ((long)b * htot + row) * D + vv * VN, part_stride, n_parts,
+                         in[r]);
     }
-    if (hh < group) Vec16<bf16>::store(sm.q + hh * D + vv * VN, out);
-    else Vec16<bf16>::store(sm.kv[hh - group] + vv * VN, out);
+  }
+  if (tid >= NT - D / 2) {
+    const int kk = tid - (NT - D / 2);
+    const float c = (-2.0f * ln_base) / (float)D;
+    const float inv = (float)exp((double)((float)kk * c));
+    float sn, cn;
+    sincosf((float)pos * inv, &sn, &cn);
+    sm.cs[kk][0] = cn;
+    sm.cs[kk][1] = sn;
+  }
+  // the table is in LDS; the barrier alone (no wait for the tile loads in
+  // flight)
+  __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
+  barrier_only();
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int i = tid + r * NT;
+    if (i < n_items) {
+      const int hh = i / (D / VN), vv = i - hh * (D / VN);
+      float out[VN];
+      if (hh <= group) {  // q and k: RoPE on the interleaved pairs
+#pragma unroll
+        for (int j = 0; j < VN / 2; ++j) {
+          const int kk = vv * (VN / 2) + j;
+          const float cn = sm.cs[kk][0], sn = sm.cs[kk][1];
+          out[2 * j] = in[r][2 * j] * cn - in[r][2 * j + 1] * sn;
+          out[2 * j + 1] = in[r][2 * j] * sn + in[r][2 * j + 1] * cn;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < VN; ++j) out[j] = in[r][j];
+      }
+      if (hh < group) Vec16<bf16>::store(sm.q + hh * D + vv * VN, out);
+      else Vec16<bf16>::store(sm.kv[hh - group] + vv * VN, out);
+    }
   }
   // q and the new k, v row are in LDS; the barrier alone (no wait for the
   // tile loads in flight)
