@@ -255,18 +255,22 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
     ksrc[i] = swz<SWZ_ROW, D>(i * 64 + lane) * 16;
     vsrc[i] = swz<SWZ_DUAL, D>(i * 64 + lane) * 16;
   }
-  // keys t0 .. t0+TK-1 (those at or past n_keys are masked)
-  auto load = [&](int t0) {
+  // K or V rows t0 .. t0+TK-1 into this wavefront's buffer (keys at or past
+  // n_keys are masked)
+  auto load_k = [&](int t0) {
     const int soff = __builtin_amdgcn_readfirstlane(t0 * D * 2);
-    char* kd = sm.u.t.k[wave];
-    char* vd = sm.u.t.v[wave];
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      dma16(krs, kd + i * 1024, ksrc[i], soff);
-      dma16(vrs, vd + i * 1024, vsrc[i], soff);
-    }
+    for (int i = 0; i < NLD; ++i) dma16(krs, sm.u.t.k[wave] + i * 1024, ksrc[i], soff);
   };
-  if (n_tiles > 0) load(k0);
+  auto load_v = [&](int t0) {
+    const int soff = __builtin_amdgcn_readfirstlane(t0 * D * 2);
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) dma16(vrs, sm.u.t.v[wave] + i * 1024, vsrc[i], soff);
+  };
+  if (n_tiles > 0) {
+    load_k(k0);
+    load_v(k0);
+  }
 
   // ---- 1. q, k, v of position pos -------------------------------------------
   // A thread sums the K-split slabs of up to two 16-byte items (group + 2
@@ -355,21 +359,20 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
   const float sl2 = scale * kLog2e;
   const char* kt = sm.u.t.k[wave];
   const char* vt = sm.u.t.v[wave];
+  // Tile it's K arrives before its V: the K of tile it + 1 is requested as
+  // soon as tile it's K fragments are in registers, its V after tile it's V
+  // reads, so the next tile's scores and softmax run while its V is still
+  // in flight (in order: K(it), V(it), then K(it + 1), V(it + 1)).
   for (int it = 0; it < n_tiles; ++it) {
     const int t0 = k0 + it * TK;
-    __builtin_amdgcn_s_waitcnt(kVmcnt0);  // tile it has landed
-    if (t0 <= pos && pos < t0 + TK) {
-      // the tile holding row pos: its k, v row from LDS (tile chunk
-      // r * CPR + c sits at LDS chunk swz(r * CPR + c)); the reads below are
-      // issued after these writes by the same wavefront
-      if (lane < 2 * CPR) {
-        const int c = lane % CPR, r = pos - t0;
-        const bool isv = lane >= CPR;
-        const u32x4 w = *reinterpret_cast<const u32x4*>(sm.kv[isv] + 8 * c);
-        char* dst = isv ? (char*)vt + swz<SWZ_DUAL, D>(r * CPR + c) * 16
-                        : (char*)kt + swz<SWZ_ROW, D>(r * CPR + c) * 16;
-        *reinterpret_cast<u32x4*>(dst) = w;
-      }
+    const bool has_pos = t0 <= pos && pos < t0 + TK;
+    // the tile holding row pos gets the new k (then v) row from LDS (tile
+    // chunk r * CPR + c sits at LDS chunk swz(r * CPR + c)); the reads below
+    // are issued after these writes by the same wavefront
+    __builtin_amdgcn_s_waitcnt(kVmWait<NLD>());  // K of tile it has landed
+    if (has_pos && lane < CPR) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(sm.kv[0] + 8 * lane);
+      *reinterpret_cast<u32x4*>((char*)kt + swz<SWZ_ROW, D>((pos - t0) * CPR + lane) * 16) = w;
     }
     u32x4 kr[DC];
 #pragma unroll
@@ -379,6 +382,9 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
     for (int cc = 0; cc < DC; ++cc) s = mfma32(as_bf16x8(kr[cc]), qreg[cc], s);
     sched_group(kDsRead, DC);
     sched_group(kMfma, DC);
+    // every K read has returned: the next tile's K may refill the buffer
+    __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
+    if (it + 1 < n_tiles) load_k(t0 + TK);
 #pragma unroll
     for (int r = 0; r < 16; ++r)
       if (t0 + 8 * (r >> 2) + 4 * g + (r & 3) >= k1) s[r] = -INFINITY;
@@ -399,6 +405,13 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
                                fast_exp2(__builtin_fmaf(s[r + 1], sl2, -m)));
       l = add_bf16x2(pb[r >> 1], l);
     }
+    // V of tile it has landed (K of tile it + 1 may still fly)
+    if (it + 1 < n_tiles) __builtin_amdgcn_s_waitcnt(kVmWait<NLD>());
+    else __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    if (has_pos && lane < CPR) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(sm.kv[1] + 8 * lane);
+      *reinterpret_cast<u32x4*>((char*)vt + swz<SWZ_DUAL, D>((pos - t0) * CPR + lane) * 16) = w;
+    }
     u32x4 va[2][DT];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
@@ -408,10 +421,10 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
         u32x2 a0 = lds_read_tr(pp + v_off[t][0]), a1 = lds_read_tr(pp + v_off[t][1]);
         va[hh][t] = u32x4{a0[0], a0[1], a1[0], a1[1]};
       }
-    // every read of the buffer has returned: the next tile may refill it
+    // every V read has returned: the next tile's V may refill the buffer
     // while the products run
     __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
-    if (it + 1 < n_tiles) load(t0 + TK);
+    if (it + 1 < n_tiles) load_v(t0 + TK);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const bf16x8 bop = as_bf16x8(u32x4{pb[4 * hh], pb[4 * hh + 1], pb[4 * hh + 2], pb[4 * hh + 3]});
