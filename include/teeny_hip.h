@@ -132,7 +132,8 @@ int teeny_flash_attn2_bwd(const void* q, const void* k, const void* v, const voi
 size_t teeny_flash_attn2_bwd_workspace_bytes(int n_ctx_q, int batch, int n_heads_q, int head_dim,
                                              int dtype);
 /* The workspace that also lets a bf16 GQA backward with few key blocks
- * (fewer 128-key blocks x batch x kv heads than two per CU) split each
+ * (fewer 128-key blocks x batch x kv heads than two per CU) and 1024 or
+ * more query rows split each
  * group's q heads over 2 or 4 dK/dV workgroups, whose fp32 partial sums a
  * merge kernel adds in a fixed order; otherwise equal to the above.  With a
  * smaller workspace the backward runs unsplit.  No counterpart in the
