@@ -159,6 +159,23 @@ def test_fa2_bf16_fwd(cuda, shape, causal):
     assert np.abs(host(lse) - le).max() <= 2e-2
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,S,D", [(1, 8, 2, 8300, 64), (1, 8, 2, 5000, 128)])
+def test_fa2_bf16_fwd_packed_long(cuda, B, Hq, Hkv, S, D):
+    """The GQA-packed causal forward (a wavefront per q head of a group of
+    4) on long sequences: D = 64 takes it at any length, D = 128 below 8000
+    rows.  The first, a middle and the last 128 query rows of every head
+    against the oracle (q_offset gives the slice its causal positions)."""
+    q, k, v, _ = inputs(80 + S, B, Hq, Hkv, S, S, D, bf16=True, spike=True)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = ops.flash_attn2_fwd(dev(q, torch.bfloat16), dev(k, torch.bfloat16),
+                                 dev(v, torch.bfloat16), scale, True)
+    o, lse = host(o), host(lse)
+    for r0 in (0, S // 2 + 5, S - 128):
+        oe, le = O.fa2_fwd(q[:, :, r0:r0 + 128], k, v, scale, True, q_offset=r0)
+        check_bf16(f"O rows {r0}+", o[:, :, r0:r0 + 128], oe)
+        assert np.abs(lse[:, :, r0:r0 + 128] - le).max() <= 2e-2
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_fa2_bf16_fwd_late_maximum(cuda, causal):
     """Rows whose maximum score lies far past their first 64-key tile: keys
