@@ -365,3 +365,12 @@ def test_fa2_bf16_c5_long_gqa(cuda, S):
     (the latter runs the dK/dV head split and its fp32 merge): one whole
     GQA group of 8 q heads."""
     _group_check(1, 64, 8, S, 128, seed=8, spike=True, groups=[(0, 5)])
+
+
+@pytest.mark.parametrize("B,S,groups", [(2, 4096, [(1, 7)]), (16, 512, [(15, 3)])])
+def test_fa2_bf16_gqa4_packed_group(cuda, B, S, groups):
+    """Causal GQA groups of 4 (Hq32 Hkv8 D128), which run the GQA-packed
+    forward and dQ: B2 S4096 (its dK/dV also splits each group's q heads
+    over two workgroups) and the Llama-3-8B prefill's B16 S512 (no split
+    below 1024 rows); one whole group each, 1% of K rows x8."""
+    _group_check(B, 32, 8, S, 128, seed=9 + S, spike=True, groups=groups)
