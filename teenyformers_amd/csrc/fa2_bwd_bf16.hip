@@ -134,36 +134,33 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
 
   // Q / dO tiles: chunk P = i*256 + tid of a tile holds tile chunk swz(P);
   // the swizzle repeats every 256 chunks.  Wave 0 also brings the rows'
-  // LSE / Delta (2*BM floats, one dword per lane).
+  // LSE / Delta (2*BM floats, one dword per lane).  The descriptors cover a
+  // whole head (rebuilt only when the walk moves to the next head) and the
+  // tile's first row is the scalar offset; rows past nq lie outside the
+  // range and load as zeros (their LSE is +inf and their dO zero, so P and
+  // dS vanish).
   const uint32_t src = swz<SWZ_DUAL, D>(tid) * 16;
+  int lhead = -1;
+  __amdgpu_buffer_rsrc_t qr, dr, lr;
   auto load_tile = [&](int head, int qb, int buf) {
-    const long bh = (long)b * hq + head0 + head;
+    if (head != lhead) {
+      const long bh = (long)b * hq + head0 + head;
+      qr = make_rsrc(q + bh * nq * D, nq * D * 2);
+      dr = make_rsrc(dout + bh * nq * D, nq * D * 2);
+      lr = make_rsrc(ld + bh * nq_pad * 2, nq_pad * 2 * 4);
+      lhead = head;
+    }
     const int row0 = qb * BM;
-    const int bytes = (nq - row0) * D * 2;  // > 0: row0 < nq
-    const auto qr = make_rsrc(q + (bh * nq + row0) * D, bytes);
-    const auto dr = make_rsrc(dout + (bh * nq + row0) * D, bytes);
     char* qdst = sm.q[buf] + wave * 1024;
     char* ddst = sm.d[buf] + wave * 1024;
-    if (row0 + BM <= nq) {
 #pragma unroll
-      for (int i = 0; i < TCH; ++i) {
-        dma16(qr, qdst + i * 4096, src + i * 4096, 0);
-        dma16(dr, ddst + i * 4096, src + i * 4096, 0);
-      }
-    } else {  // rows past nq re-read row nq - 1 (their LSE is +inf: P = 0)
-      const int lastrow = nq - 1 - row0;
-#pragma unroll
-      for (int i = 0; i < TCH; ++i) {
-        const int o = src + i * 4096;
-        const int oc = min(o / (2 * D), lastrow) * (2 * D) + o % (2 * D);
-        dma16(qr, qdst + i * 4096, oc, 0);
-        dma16(dr, ddst + i * 4096, oc, 0);
-      }
+    for (int i = 0; i < TCH; ++i) {
+      dma16(qr, qdst + i * 4096, src + i * 4096, row0 * D * 2);
+      dma16(dr, ddst + i * 4096, src + i * 4096, row0 * D * 2);
     }
-    if (wave == 0) {
-      const auto lr = make_rsrc(ld + (bh * nq_pad + row0) * 2, 2 * BM * 4);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(lr, (lds_void*)sm.ld[buf], 4, lane * 4, 0, 0, 0);
-    }
+    if (wave == 0)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(lr, (lds_void*)sm.ld[buf], 4, lane * 4,
+                                               row0 * 2 * 4, 0, 0);
   };
 
   // ---- LDS read offsets (bytes) --------------------------------------------
@@ -202,6 +199,9 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
   __builtin_amdgcn_s_waitcnt(0);  // V block and the first tile
   __syncthreads();
 
+  // one Q/dO tile; its buffer `buf` (= it % 2) is a constant in each of the
+  // two unrolled steps, so every LDS address is a lane offset plus an
+  // immediate
   for (int it = 0; it < n_iter; ++it) {
     const int buf = it & 1;
     const int qb0 = qb * BM;
