@@ -143,6 +143,8 @@ BF16_SHAPES = [  # B, Hq, Hkv, Sq, Sk, D
     (2, 8, 2, 200, 260, 64),    # causal: GQA 4 packed (a wavefront per q head), Sq < Sk
     (1, 8, 2, 300, 100, 64),    # GQA 4 packed, Sq > Sk
     (1, 16, 2, 333, 333, 128),  # GQA 8 packed
+    (1, 4, 1, 1, 100, 64),      # GQA 4 packed, one query row
+    (2, 8, 2, 33, 70, 128),     # GQA 4 packed, one row past a 32-row block
 ]
 
 
