@@ -8,9 +8,17 @@
  * an optional workspace, and the HIP stream all work is queued on.
  *
  * Conventions
- *   - Every pointer is device memory owned by the caller.  Functions never
- *     allocate device memory, never synchronise the device, and return as
- *     soon as the work is queued on `stream` (0 = the null stream).
+ *   - Every pointer is device memory owned by the caller.  Work buffers are
+ *     the caller's too: an entry point that needs one takes a workspace
+ *     argument whose size a *_workspace_bytes query gives.  Functions never
+ *     synchronise the device and return as soon as the work is queued on
+ *     `stream` (0 = the null stream).
+ *   - Set-up allocates, the calls after it do not: teeny_init (or the first
+ *     call on a device) loads this library's code objects there, and
+ *     teeny_linear_bf16 / teeny_linear_f32 create a hipBLASLt handle per
+ *     device and a plan per product shape at a shape's first call (no
+ *     workspace: hipBLASLt runs only algorithms that need none).  Call
+ *     teeny_init and each product shape once before capturing a HIP graph.
  *   - Layouts are the reference's: attention tensors [B*H, S, D] contiguous
  *     (src/kernels/flash_attn2.rs:23), activations [rows, cols] row-major.
  *   - dtype is TEENY_F32 (the reference's type) or TEENY_BF16 (storage; all
@@ -55,13 +63,17 @@ typedef enum { TEENY_F32 = 0, TEENY_BF16 = 1, TEENY_I32 = 2 } teeny_dtype;
 #define TEENY_ERR_MODULE (-6)         /* code object or kernel symbol could not be loaded */
 #define TEENY_ERR_INVALID_VALUE (-7)  /* a scalar argument is out of its domain */
 #define TEENY_ERR_SCRATCH (-8)        /* needs more than the static scratch array (noalloc) */
+#define TEENY_ERR_NOT_INITIALIZED (-9) /* teeny_init has not run on the device (noalloc) */
 
 /* Library version, error text, last HIP error seen by this thread. */
 int teeny_abi_version(void);
 const char* teeny_strerror(int code);
 int teeny_last_hip_error(void);
 
-/* Load the code objects on the current device (optional: done lazily). */
+/* Load the code objects on the current device and look up the address of
+ * the no-allocation backward's scratch array there.  Optional for every
+ * other entry point (they load lazily); required, once per device, before
+ * teeny_causal_flash_attn2_bwd_noalloc. */
 int teeny_init(void);
 
 /* Launch profiler (no counterpart in the reference, which has no tracing).
@@ -146,11 +158,13 @@ size_t teeny_flash_attn2_bwd_workspace_bytes_gqa(int n_ctx_q, int n_ctx_k, int b
  * that cannot allocate device memory (code under HIP graph capture, serving
  * loops, harnesses that forbid hipMalloc).  The workspace is a static device
  * array of this library, teeny_scratch_bytes() (16 MiB) per device, held until
- * the process ends; its address is looked up once per device (teeny_init or
- * the first call).  Problems whose teeny_flash_attn2_bwd_workspace_bytes
- * exceed it return TEENY_ERR_SCRATCH (B*Hq*ceil32(n_ctx_q)*8 bytes for bf16:
- * e.g. B8 Hq32 S4096 needs 8 MiB).  A GQA split runs when it fits in the
- * array.  Calls no allocating routine.  Every call on a device shares that
+ * the process ends; its address is looked up by teeny_init, which must have
+ * run on the device (else TEENY_ERR_NOT_INITIALIZED: this entry point loads
+ * and looks up nothing itself).  Problems whose
+ * teeny_flash_attn2_bwd_workspace_bytes exceed it return TEENY_ERR_SCRATCH
+ * (B*Hq*ceil32(n_ctx_q)*8 bytes for bf16: e.g. B8 Hq32 S4096 needs 8 MiB).
+ * A GQA split runs when it fits in the array.  Calls no allocating routine
+ * and may be captured in a HIP graph.  Every call on a device shares that
  * device's array: calls that overlap on one device (other streams or
  * threads) race.  Arguments otherwise as teeny_causal_flash_attn2_bwd. */
 size_t teeny_scratch_bytes(void);
@@ -302,15 +316,16 @@ int teeny_decode_attention_dev(const void* q, const void* k_cache, const void* v
 int teeny_argmax_rows(const void* x, int64_t* out, int rows, int cols, int dtype,
                       hipStream_t stream);
 
-/* Linear layer y[M, N] = x[M, K] . w[N, K]^T, bf16 only, any M >= 1: replaces
+/* Linear layer y[M, N] = x[M, K] . w[N, K]^T in bf16, any M >= 1: replaces
  * the external teeny-core Linear behind sym_linear (src/layers/mod.rs:54-58).
  * Up to 16 rows (a KV-cached decode step) with N % 128 == 0 and K % 128 == 0
  * stream the weight through a GEMV-shaped kernel; more rows go to hipBLASLt
  * (faster than this library's GEMM at the Llama prompt shapes), and to
- * teeny_gemm_bf16 where hipBLASLt does not take the device or shape; both
- * require N % 64 == 0 and K % 64 == 0 (otherwise TEENY_ERR_UNSUPPORTED).
- * Every path accumulates in fp32 and rounds each output to bf16 once; the
- * hipBLASLt path keeps a workspace per (device, stream).
+ * teeny_gemm_bf16 where hipBLASLt does not take the device or shape or the
+ * stream is capturing (a fixed rule: a captured product never runs
+ * hipBLASLt); both require N % 64 == 0 and K % 64 == 0 (otherwise
+ * TEENY_ERR_UNSUPPORTED).  Every path accumulates in fp32 and rounds each
+ * output to bf16 once; none uses a workspace.
  * teeny_linear_swiglu_bf16: w is the fused gate_up weight [2F, K] (gate rows
  * first, src/loader.rs:49-55); writes y[M, F] = silu(x w_gate^T) *
  * (x w_up^T) with both products rounded to bf16 first, as FeedForward's
@@ -329,6 +344,19 @@ int teeny_gemm_bf16(const void* x, const void* w, void* y, int M, int N, int K,
                     hipStream_t stream);
 int teeny_linear_swiglu_bf16(const void* x, const void* w, void* y, int M, int F, int K,
                              hipStream_t stream);
+
+/* The same Linear in fp32, the reference's precision (teeny-core's Linear
+ * behind sym_linear, src/layers/mod.rs:54-58, on the f32 weights that
+ * src/loader.rs:41,66-80 decodes): hipBLASLt's fp32 GEMM (fp32 products
+ * and accumulation, no workspace), or teeny_gemm_f32 where hipBLASLt does
+ * not take the device or shape or the stream is capturing.  Any M and N; K
+ * a multiple of 4; x and w 16-byte aligned. */
+int teeny_linear_f32(const void* x, const void* w, void* y, int M, int N, int K,
+                     hipStream_t stream);
+/* This library's fp32 GEMM for the same product: each output one fp32
+ * fused multiply-add chain over k in increasing order. */
+int teeny_gemm_f32(const void* x, const void* w, void* y, int M, int N, int K,
+                   hipStream_t stream);
 
 /* The same product split over K for more parallelism at small N: writes
  * teeny_linear_partials_count(K, k_split) fp32 slabs parts[n][M][N], slab i

@@ -20,6 +20,8 @@
  * Pinning (how each function is checked; see tests/test_oracle.py):
  *   orc_rope               reference fixture tests/golden/rope (1e-4, the
  *                          reference's own tolerance) + closed form + R(-t)R(t)=I
+ *   orc_rope_at            bit-equal to orc_rope on rows padded to start at pos0,
+ *                          + the float64 closed form at positions past 500
  *   orc_swiglu_fwd         reference fixture tests/golden/swiglu
  *   orc_swiglu_bwd         fp64 central finite differences
  *   orc_fused_add_rmsnorm_fwd  reference fixture tests/golden/fused_add_rmsnorm (y and h)
@@ -332,20 +334,21 @@ EXPORT float orc_rope_inv_freq(int k, int d, float ln_base) {
 
 /*
  * rope_forward (src/kernels/rope.rs:57-97) and rope_backward (:104-140) on
- * x [BH, N_CTX, HEAD_DIM]; position = row index within a BH slice (:68-71).
+ * x [BH, N_CTX, HEAD_DIM]; position = row index within a BH slice (:68-71),
+ * plus pos0 (0 in the reference; a KV-cached step's rows start later).
  *   fwd: y[2k] = x0 cos - x1 sin,  y[2k+1] = x0 sin + x1 cos      (:95-96)
  *   bwd: dx[2k] = dy0 cos + dy1 sin, dx[2k+1] = -dy0 sin + dy1 cos (:138-139)
  * theta = fp32(pos) * inv_freq; cos/sin are correctly rounded (double
  * evaluation rounded to fp32).
  */
-EXPORT void orc_rope(const float* x, float* y, int bh, int n_ctx, int d, float ln_base,
-                     int backward) {
+EXPORT void orc_rope_at(const float* x, float* y, int bh, int n_ctx, int d, float ln_base,
+                        int backward, int pos0) {
   const int half = d / 2;
   float* inv = (float*)malloc(sizeof(float) * half);
   for (int kk = 0; kk < half; ++kk) inv[kk] = orc_rope_inv_freq(kk, d, ln_base);
 #pragma omp parallel for schedule(static)
   for (long r = 0; r < (long)bh * n_ctx; ++r) {
-    int pos = (int)(r % n_ctx);
+    int pos = pos0 + (int)(r % n_ctx);
     const float* xr = x + (size_t)r * d;
     float* yr = y + (size_t)r * d;
     for (int kk = 0; kk < half; ++kk) {
@@ -363,6 +366,11 @@ EXPORT void orc_rope(const float* x, float* y, int bh, int n_ctx, int d, float l
     }
   }
   free(inv);
+}
+
+EXPORT void orc_rope(const float* x, float* y, int bh, int n_ctx, int d, float ln_base,
+                     int backward) {
+  orc_rope_at(x, y, bh, n_ctx, d, ln_base, backward, 0);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -44,6 +44,7 @@ def lib():
         L.orc_rope_inv_freq.argtypes = [_I, _I, ctypes.c_float]
         L.orc_rope_inv_freq.restype = ctypes.c_float
         L.orc_rope.argtypes = [_F, _F, _I, _I, _I, ctypes.c_float, _I]
+        L.orc_rope_at.argtypes = [_F, _F, _I, _I, _I, ctypes.c_float, _I, _I]
         L.orc_transpose_heads.argtypes = [_V, _V, _I, _I, _I, _I, _I, _I]
         L.orc_fused_add_rmsnorm_fwd.argtypes = [_F] * 6 + [_I, _I, ctypes.c_float]
         L.orc_rmsnorm_fwd.argtypes = [_F] * 4 + [_I, _I, ctypes.c_float]
@@ -161,13 +162,17 @@ def rope_inv_freq(d: int, ln_base: float) -> np.ndarray:
     return np.array([lib().orc_rope_inv_freq(k, d, ln_base) for k in range(d // 2)], np.float32)
 
 
-def rope(x, ln_base: float, backward: bool = False) -> np.ndarray:
-    """x [..., S, D] (leading dims flattened to BH) -> rotated copy (fp32)."""
+def rope(x, ln_base: float, backward: bool = False, pos0: int = 0) -> np.ndarray:
+    """x [..., S, D] (leading dims flattened to BH) -> rotated copy (fp32);
+    row s of each slice at position pos0 + s."""
     x, px = _f32(x)
     S, D = x.shape[-2], x.shape[-1]
     bh = int(np.prod(x.shape[:-2])) if x.ndim > 2 else 1
     y = np.empty_like(x)
-    lib().orc_rope(px, _pf(y), bh, S, D, float(ln_base), int(backward))
+    if pos0:
+        lib().orc_rope_at(px, _pf(y), bh, S, D, float(ln_base), int(backward), int(pos0))
+    else:
+        lib().orc_rope(px, _pf(y), bh, S, D, float(ln_base), int(backward))
     return y
 
 

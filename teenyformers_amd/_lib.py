@@ -76,6 +76,8 @@ _SIGNATURES = {
     "teeny_linear_bf16": ([_p, _p, _p, _i, _i, _i, _p], _i),
     "teeny_gemm_bf16": ([_p, _p, _p, _i, _i, _i, _p], _i),
     "teeny_linear_swiglu_bf16": ([_p, _p, _p, _i, _i, _i, _p], _i),
+    "teeny_linear_f32": ([_p, _p, _p, _i, _i, _i, _p], _i),
+    "teeny_gemm_f32": ([_p, _p, _p, _i, _i, _i, _p], _i),
     "teeny_linear_partials_count": ([_i, _i], _i),
     "teeny_linear_partials_bf16": ([_p, _p, _p, _i, _i, _i, _i, _p], _i),
     "teeny_fused_add_rmsnorm_partials_fwd": ([_p, _i, _p, _p, _p, _p, _p, _i, _i, _f, _i, _p], _i),

@@ -37,7 +37,7 @@ ARCH = "gfx950"
 # Order matters only for readability; capi.cpp declares the same list.
 KERNEL_SOURCES = [
     "transpose", "rope", "norm", "swiglu", "embed", "fa2_f32", "fa2_fwd_bf16", "fa2_bwd_bf16",
-    "llama", "decode_bf16", "linear_bf16", "gemm_bf16",
+    "llama", "decode_bf16", "linear_bf16", "gemm_bf16", "gemm_f32",
 ]
 
 HIPCC_FLAGS = [

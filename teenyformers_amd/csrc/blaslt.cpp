@@ -1,20 +1,28 @@
-// Prompt-size bf16 linear layers through hipBLASLt, the vendor GEMM library.
+// Prompt-size linear layers through hipBLASLt, the vendor GEMM library.
 //
-// y[M, N] = x[M, K] . w[N, K]^T, fp32 accumulation, y rounded to bf16 once:
-// the same product as gemm_bf16.hip.  At the Llama shapes the library picks
-// kernels with 128 x 128 wavefront tiles (one wavefront per SIMD) that keep
-// the matrix cores busier than this library's own GEMM (0.80 against 0.65 of
-// the cycles, measured), so teeny_linear_bf16 hands its plain products of
-// more than 16 rows here and keeps its own kernel as the fallback (and for
-// the fused SwiGLU product, which hipBLASLt has no epilogue for).
+// y[M, N] = x[M, K] . w[N, K]^T with fp32 accumulation, y stored once in the
+// operands' type (bf16 or fp32): the same product as gemm_bf16.hip /
+// gemm_f32.hip.  At the Llama shapes the library picks kernels with
+// 128 x 128 wavefront tiles (one wavefront per SIMD) that keep the matrix
+// cores busier than this library's own GEMM (0.80 against 0.65 of the
+// cycles, measured), so teeny_linear_bf16 hands its plain products of more
+// than 16 rows here and keeps its own kernel as the fallback (and for the
+// fused SwiGLU product, which hipBLASLt has no epilogue for).
 //
 // In hipBLASLt's column-major terms y^T [N, M] = W [N, K] . x^T [K, M]: A is
 // the weight's memory read as a K x N column-major matrix and transposed, B
 // the activations' memory as a K x M column-major matrix, D y's memory as an
-// N x M column-major matrix.  Plans (descriptors and the heuristic's first
-// algorithm) are cached per (device, M, N, K); each (device, stream) gets
-// its own workspace, so products on different streams never share one.  The
-// handle, plans and workspaces live until the process ends.
+// N x M column-major matrix.
+//
+// No workspace: the heuristic is asked for algorithms that need none (at the
+// Llama prompt shapes they run within 1 % of those it picks under a 64 MiB
+// limit, measured), so a product never allocates device memory and products
+// on different streams or threads share nothing but the read-only plan.
+// Plans (descriptors and the heuristic's first algorithm) are built once per
+// (device, dtype, M, N, K) under a lock and never freed; the matmul itself is
+// enqueued outside the lock.  Under stream capture nothing is built or run
+// here (the caller's own GEMM runs instead), so which GEMM a captured graph
+// holds does not depend on what ran before the capture.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -24,8 +32,6 @@
 #include <tuple>
 
 namespace {
-
-constexpr size_t kWorkspace = 64u << 20;  // bytes per (device, stream)
 
 struct Plan {
   bool ok = false;
@@ -37,27 +43,27 @@ struct Plan {
 struct Device {
   bool tried = false;
   hipblasLtHandle_t handle = nullptr;
-  std::map<std::tuple<int, int, int>, Plan> plans;
-  std::map<hipStream_t, void*> workspace;
+  // std::map: a plan's address stays valid while other plans are added
+  std::map<std::tuple<int, int, int, int>, Plan> plans;
 };
 
 std::mutex mu;
 std::map<int, Device> devices;
 
-Plan make_plan(hipblasLtHandle_t h, int M, int N, int K) {
+Plan make_plan(hipblasLtHandle_t h, hipDataType t, int M, int N, int K) {
   Plan p;
   const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
   if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
     return p;
   hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta);
   hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb);
-  if (hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, K, N, K) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, K, M, K) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatrixLayoutCreate(&p.d, HIP_R_16BF, N, M, N) != HIPBLAS_STATUS_SUCCESS)
+  if (hipblasLtMatrixLayoutCreate(&p.a, t, K, N, K) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&p.b, t, K, M, K) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&p.d, t, N, M, N) != HIPBLAS_STATUS_SUCCESS)
     return p;
   hipblasLtMatmulPreference_t pref = nullptr;
   if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return p;
-  const uint64_t max_ws = kWorkspace;
+  const uint64_t max_ws = 0;
   hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &max_ws,
                                         sizeof max_ws);
   hipblasLtMatmulHeuristicResult_t res[1];
@@ -66,52 +72,53 @@ Plan make_plan(hipblasLtHandle_t h, int M, int N, int K) {
       hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.a, p.b, p.d, p.d, pref, 1, res, &n);
   hipblasLtMatmulPreferenceDestroy(pref);
   if (s != HIPBLAS_STATUS_SUCCESS || n < 1 || res[0].state != HIPBLAS_STATUS_SUCCESS) return p;
-  if (res[0].workspaceSize > kWorkspace) return p;
+  if (res[0].workspaceSize != 0) return p;
   p.algo = res[0].algo;
   p.ok = true;
   return p;
 }
 
-}  // namespace
-
-// 0: y written (launched on `stream`); -1: hipBLASLt is not available for
-// this device or shape, nothing was launched (the caller uses its own GEMM).
-extern "C" __attribute__((visibility("hidden"))) int teeny_lt_gemm_bf16(
-    const void* x, const void* w, void* y, int M, int N, int K, hipStream_t stream) {
+// 0: y written (launched on `stream`); -1: hipBLASLt is not used for this
+// device, shape or stream state, nothing was launched.
+int lt_gemm(hipDataType t, const void* x, const void* w, void* y, int M, int N, int K,
+            hipStream_t stream) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return -1;
-  // under stream capture nothing is created (handle, plan, workspace): a
-  // shape met first inside a capture runs the caller's own GEMM
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return -1;
-  const bool capturing = cap != hipStreamCaptureStatusNone;
-  std::lock_guard<std::mutex> lock(mu);
-  Device& d = devices[dev];
-  if (!d.tried) {
-    if (capturing) return -1;
-    d.tried = true;
-    if (hipblasLtCreate(&d.handle) != HIPBLAS_STATUS_SUCCESS) d.handle = nullptr;
-  }
-  if (!d.handle) return -1;
-  auto key = std::make_tuple(M, N, K);
-  auto it = d.plans.find(key);
-  if (it == d.plans.end()) {
-    if (capturing) return -1;
-    it = d.plans.emplace(key, make_plan(d.handle, M, N, K)).first;
-  }
-  const Plan& p = it->second;
-  if (!p.ok) return -1;
-  // the whole workspace goes with every call (the heuristic chose its
-  // algorithm under that limit)
-  auto wi = d.workspace.find(stream);
-  if (wi == d.workspace.end()) {
-    if (capturing) return -1;
-    void* buf = nullptr;
-    if (hipMalloc(&buf, kWorkspace) != hipSuccess) return -1;
-    wi = d.workspace.emplace(stream, buf).first;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+    return -1;
+  hipblasLtHandle_t handle = nullptr;
+  const Plan* plan = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    Device& d = devices[dev];
+    if (!d.tried) {
+      d.tried = true;
+      if (hipblasLtCreate(&d.handle) != HIPBLAS_STATUS_SUCCESS) d.handle = nullptr;
+    }
+    if (!d.handle) return -1;
+    auto key = std::make_tuple((int)t, M, N, K);
+    auto it = d.plans.find(key);
+    if (it == d.plans.end()) it = d.plans.emplace(key, make_plan(d.handle, t, M, N, K)).first;
+    if (!it->second.ok) return -1;
+    handle = d.handle;
+    plan = &it->second;
   }
   const float alpha = 1.0f, beta = 0.0f;
-  const hipblasStatus_t s = hipblasLtMatmul(d.handle, p.desc, &alpha, w, p.a, x, p.b, &beta, y,
-                                            p.d, y, p.d, &p.algo, wi->second, kWorkspace, stream);
+  const hipblasStatus_t s = hipblasLtMatmul(handle, plan->desc, &alpha, w, plan->a, x, plan->b,
+                                            &beta, y, plan->d, y, plan->d, &plan->algo, nullptr,
+                                            0, stream);
   return s == HIPBLAS_STATUS_SUCCESS ? 0 : -1;
+}
+
+}  // namespace
+
+extern "C" __attribute__((visibility("hidden"))) int teeny_lt_gemm_bf16(
+    const void* x, const void* w, void* y, int M, int N, int K, hipStream_t stream) {
+  return lt_gemm(HIP_R_16BF, x, w, y, M, N, K, stream);
+}
+
+extern "C" __attribute__((visibility("hidden"))) int teeny_lt_gemm_f32(
+    const void* x, const void* w, void* y, int M, int N, int K, hipStream_t stream) {
+  return lt_gemm(HIP_R_32F, x, w, y, M, N, K, stream);
 }

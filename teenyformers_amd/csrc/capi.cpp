@@ -36,12 +36,15 @@
   X(llama)               \
   X(decode_bf16)         \
   X(linear_bf16)         \
-  X(gemm_bf16)
+  X(gemm_bf16)           \
+  X(gemm_f32)
 
 // noalloc.hip: the current device's address of its static scratch array
 extern "C" __attribute__((visibility("hidden"))) int teeny_scratch_setup(void** out);
-// blaslt.cpp: a prompt-size product through hipBLASLt (0), or -1 to fall back
+// blaslt.cpp: a product through hipBLASLt (0), or -1 to fall back
 extern "C" __attribute__((visibility("hidden"))) int teeny_lt_gemm_bf16(
+    const void* x, const void* w, void* y, int M, int N, int K, hipStream_t stream);
+extern "C" __attribute__((visibility("hidden"))) int teeny_lt_gemm_f32(
     const void* x, const void* w, void* y, int M, int N, int K, hipStream_t stream);
 
 #define TEENY_CO_DECL(n) \
@@ -95,6 +98,14 @@ int load_device_locked(int dev, DeviceState** out) {
   g_dev[dev] = st;
   *out = st;
   return TEENY_OK;
+}
+
+// Whether the current device's code objects are loaded (loads nothing).
+bool device_ready() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lk(g_mu);
+  return g_dev[dev] != nullptr;
 }
 
 int get_function(const char* name, hipFunction_t* fn) {
@@ -209,9 +220,11 @@ int fa2_check(const void* q, const void* k, const void* v, int n_ctx_q, int n_ct
       (long)batch * hkv * n_ctx_k * head_dim >= kMaxElems)
     return TEENY_ERR_INVALID_SHAPE;
   if (!fa2_head_dim_ok(head_dim, dtype)) return TEENY_ERR_UNSUPPORTED;
-  // bf16 kernels address one head's K / V through a buffer descriptor whose
-  // byte range is a signed 32-bit kernel argument
-  if (dtype == TEENY_BF16 && (long)n_ctx_k * head_dim * 2 >= kMaxElems)
+  // bf16 kernels address one head's rows through buffer descriptors whose
+  // byte ranges and tile offsets are signed 32-bit values: K / V in every
+  // kernel, Q and dO in the dK/dV kernel
+  if (dtype == TEENY_BF16 &&
+      ((long)n_ctx_k * head_dim * 2 >= kMaxElems || (long)n_ctx_q * head_dim * 2 >= kMaxElems))
     return TEENY_ERR_INVALID_SHAPE;
   return TEENY_OK;
 }
@@ -437,6 +450,7 @@ const char* teeny_strerror(int code) {
     case TEENY_ERR_MODULE: return "code object or kernel could not be loaded";
     case TEENY_ERR_INVALID_VALUE: return "invalid scalar argument";
     case TEENY_ERR_SCRATCH: return "problem needs more than the library's static scratch array";
+    case TEENY_ERR_NOT_INITIALIZED: return "teeny_init has not run on the current device";
     default: return "unknown error";
   }
 }
@@ -452,14 +466,13 @@ int teeny_init(void) {
     int rc = load_device_locked(dev, &st);
     if (rc) return rc;
   }
-  // this device's address of the no-allocation entry point's scratch array;
-  // a failure here is reported by that entry point (it asks again), not by
-  // the rest of the library
-  (void)teeny_scratch_setup(nullptr);
-  return TEENY_OK;
+  // this device's address of the no-allocation entry point's scratch array,
+  // asked here once so that entry point never loads or looks anything up
+  return teeny_scratch_setup(nullptr);
 }
 
 __attribute__((visibility("hidden"))) void teeny_set_last_hip_error(int e) { g_last_hip = e; }
+__attribute__((visibility("hidden"))) int teeny_device_ready(void) { return device_ready(); }
 
 int teeny_profile_enable(int on) {
   std::lock_guard<std::mutex> lk(g_prof_mu);
@@ -853,8 +866,10 @@ int teeny_decode_qkv_attention_dev(const float* parts, int n_parts, void* k_cach
   if (n_heads_q / n_heads_kv > 32) return TEENY_ERR_UNSUPPORTED;
   const int htot = n_heads_q + 2 * n_heads_kv;
   long part_stride = (long)batch * htot * head_dim;
+  // the kernel addresses one (b, kv head) cache slab with 32-bit byte offsets
   if (part_stride * n_parts >= kMaxElems ||
-      (long)batch * n_heads_kv * cache_len * head_dim >= kMaxElems)
+      (long)batch * n_heads_kv * cache_len * head_dim >= kMaxElems ||
+      (long)cache_len * head_dim * 2 >= kMaxElems)
     return TEENY_ERR_INVALID_SHAPE;
   if (!std::isfinite(ln_rope_base) || !scale_ok(softmax_scale, dtype))
     return TEENY_ERR_INVALID_VALUE;
@@ -1012,6 +1027,39 @@ int teeny_linear_bf16(const void* x, const void* w, void* y, int M, int N, int K
   if ((long)K * 2 * 256 >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
   if (M > 16 && teeny_lt_gemm_bf16(x, w, y, M, N, K, stream) == 0) return TEENY_OK;
   return teeny_gemm_bf16(x, w, y, M, N, K, stream);
+}
+
+// fp32 products (the reference's precision): this library's fp32 GEMM
+// (gemm_f32.hip: 128 x 128 tiles of y, 256 threads), any M and N, K a
+// multiple of 4, 16-byte aligned x and w.
+static int gemm_f32_check(const void* x, const void* w, const void* y, int M, int N, int K) {
+  if (!x || !w || !y) return TEENY_ERR_NULL_POINTER;
+  if (M <= 0 || N <= 0 || K <= 0 || (long)N * K >= kMaxElems * 2 ||
+      (long)M * K >= kMaxElems * 2 || (long)M * N >= kMaxElems * 2)
+    return TEENY_ERR_INVALID_SHAPE;
+  if (K % 4 != 0) return TEENY_ERR_UNSUPPORTED;
+  if (((uintptr_t)x | (uintptr_t)w) % 16 != 0) return TEENY_ERR_INVALID_VALUE;
+  if ((M + 127) / 128 > 65535) return TEENY_ERR_INVALID_SHAPE;
+  return TEENY_OK;
+}
+
+int teeny_gemm_f32(const void* x, const void* w, void* y, int M, int N, int K,
+                   hipStream_t stream) {
+  int rc = gemm_f32_check(x, w, y, M, N, K);
+  if (rc) return rc;
+  void* args[] = {&x, &w, &y, &M, &N, &K};
+  return launch("teeny_gemm_f32_nt", dim3((N + 127) / 128, (M + 127) / 128), dim3(256), 0, stream,
+                args);
+}
+
+// hipBLASLt's fp32 GEMM (no workspace), or teeny_gemm_f32 where hipBLASLt
+// does not take the device or shape, or the stream is capturing.
+int teeny_linear_f32(const void* x, const void* w, void* y, int M, int N, int K,
+                     hipStream_t stream) {
+  int rc = gemm_f32_check(x, w, y, M, N, K);
+  if (rc) return rc;
+  if (teeny_lt_gemm_f32(x, w, y, M, N, K, stream) == 0) return TEENY_OK;
+  return teeny_gemm_f32(x, w, y, M, N, K, stream);
 }
 
 // Any M, as teeny_linear_bf16: up to 16 rows through linear_bf16.hip's

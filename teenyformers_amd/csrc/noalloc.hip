@@ -7,8 +7,11 @@
 // only `scratch`; the HIP runtime gives each device its own copy of the array
 // when it loads this file's code object, and hipGetSymbolAddress returns that
 // device's address.  That address, never the host-side name `scratch`, is
-// what reaches kernels.  Every call on a device shares its array: calls that
-// overlap on one device (two streams, two threads) race on it.  Nothing in
+// what reaches kernels; teeny_init asks for it on each device, and the entry
+// point refuses a device where that has not happened
+// (TEENY_ERR_NOT_INITIALIZED) rather than loading anything itself.  Every
+// call on a device shares its array: calls that overlap on one device (two
+// streams, two threads) race on it.  Nothing in
 // the array has to start at zero: the dQ kernel writes every LSE / Delta slot
 // (padding included) before the dK/dV kernel reads it, and split partial sums
 // are written whole before the merge reads them.
@@ -18,8 +21,10 @@
 
 #include "teeny_hip.h"
 
-// capi.cpp: records a failed HIP call for teeny_last_hip_error
+// capi.cpp: records a failed HIP call for teeny_last_hip_error; whether the
+// current device's code objects are loaded (teeny_init has run on it)
 extern "C" __attribute__((visibility("hidden"))) void teeny_set_last_hip_error(int e);
+extern "C" __attribute__((visibility("hidden"))) int teeny_device_ready(void);
 
 namespace {
 
@@ -34,7 +39,7 @@ void* g_scratch_ptr[kMaxDevices] = {};
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 // The current device's address of `scratch`, asked once per device with that
-// device current (teeny_init, or the first call on the device).
+// device current, from teeny_init.
 extern "C" __attribute__((visibility("hidden"))) int teeny_scratch_setup(void** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -71,9 +76,22 @@ int teeny_causal_flash_attn2_bwd_noalloc(const void* q, const void* k, const voi
   const size_t need =
       teeny_flash_attn2_bwd_workspace_bytes(n_ctx_q, batch, n_heads_q, head_dim, dtype);
   if (need > kScratchBytes) return TEENY_ERR_SCRATCH;
+  // set up by teeny_init on this device, or refused: loading code objects or
+  // asking for the array's address here would allocate and synchronise,
+  // which is what this entry point's callers (graph capture) cannot have
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    teeny_set_last_hip_error((int)e);
+    return TEENY_ERR_HIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return TEENY_ERR_HIP;
   void* ws = nullptr;
-  int rc = teeny_scratch_setup(&ws);
-  if (rc) return rc;
+  {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    ws = g_scratch_ptr[dev];
+  }
+  if (!ws || !teeny_device_ready()) return TEENY_ERR_NOT_INITIALIZED;
   // the whole array: a GQA split that fits in it is used, as the allocating
   // entry point does with a workspace of this size
   return teeny_causal_flash_attn2_bwd(q, k, v, o, dout, l, dq, dk, dv, n_ctx_q, n_ctx_k,

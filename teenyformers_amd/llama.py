@@ -21,11 +21,14 @@ MI355X-specific structure (same arithmetic):
   * prefill runs the causal FA2 kernel over the cache; each decode step runs
     teeny_decode_attention over the cached keys;
   * Linear layers (teeny-core's external `Linear`, src/layers/mod.rs:54-58,
-    y = x W^T with W [out, in]) are this library's kernels: the matrix-core
-    GEMM for a prompt, and with at most 16 rows (a decode step) the
+    y = x W^T with W [out, in]) run through the library's linear entry
+    points: a prompt's products through hipBLASLt (teeny_linear_bf16 /
+    teeny_linear_f32), and with at most 16 rows (a decode step) the
     weight-streaming kernels: gate_up fused with SwiGLU, and q|k|v, o and
     down split over K into fp32 slabs that the QKV split and the
-    residual-add norms sum.
+    residual-add norms sum.  Decode steps of more than 16 sequences run the
+    library's own GEMM (ops.own_gemm), the kernel a captured graph runs, so
+    eager and graph-replayed steps compute the same bits.
 """
 from __future__ import annotations
 
@@ -291,8 +294,9 @@ class Llama:
 
     def decode_step(self, cache: KVCache, ids: torch.Tensor) -> torch.Tensor:
         """One token per sequence (ids [B, 1]) -> next-token logits [B, vocab]."""
-        h = self.hidden(ids, cache, cache.length)
-        return self.logits(h[:, -1])
+        with ops.own_gemm():  # the kernels of the graph-captured step
+            h = self.hidden(ids, cache, cache.length)
+            return self.logits(h[:, -1])
 
     def generate(self, prompt: torch.Tensor, n_new: int) -> torch.Tensor:
         """Greedy decoding with the KV cache -> generated ids [B, n_new]."""
@@ -367,10 +371,15 @@ class DecodeGraph:
     from `pos` (int32, device); replay() writes the next ids into `ids`,
     appends one cache row and advances `pos`.  The constructor runs the first
     step eagerly on a side stream (the capture needs its libraries warmed up)
-    and then captures it, so after construction `ids` holds step 1's output.
-    Positions past the cache capacity are not written (the kernels check)."""
+    and then captures it, so after construction `ids` holds step 1's output
+    and `first_logits` its logits.  `logits` [B, vocab] holds the last
+    replayed step's logits.  trace: a list that the captured step's blocks
+    append their sub-layer tensors to (as Llama.hidden's trace); after each
+    replay they hold that step's values.  Positions past the cache capacity
+    are not written (the kernels check)."""
 
-    def __init__(self, model: Llama, cache: KVCache, ids: torch.Tensor):
+    def __init__(self, model: Llama, cache: KVCache, ids: torch.Tensor,
+                 trace: list | None = None):
         self.model, self.cache = model, cache
         self.ids = ids.to(torch.int64).clone()
         self.pos = torch.full((1,), cache.length, dtype=torch.int32, device=ids.device)
@@ -381,17 +390,22 @@ class DecodeGraph:
             self._step()
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
+        self.first_logits = self.logits
         cache.length += 1
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self._step()
+            self._step(trace)
 
-    def _step(self):
+    def _step(self, trace: list | None = None):
         m = self.model
-        h = m.hidden(self.ids, self.cache, self.pos)
-        # the greedy choice lands in the ids the next replay embeds (the
-        # embedding read them at the start of this step)
-        ops.argmax_rows(m.logits(h[:, -1]), out=self.ids.view(-1))
+        # the eager first step runs the kernels the capture records (above 16
+        # sequences the library's own GEMM, as teeny_linear_bf16 under capture)
+        with ops.own_gemm():
+            h = m.hidden(self.ids, self.cache, self.pos, trace=trace)
+            self.logits = m.logits(h[:, -1])
+            # the greedy choice lands in the ids the next replay embeds (the
+            # embedding read them at the start of this step)
+            ops.argmax_rows(self.logits, out=self.ids.view(-1))
         self.pos.add_(1)
 
     def replay(self):

@@ -8,7 +8,9 @@ Shapes follow the reference with the batch split out:
 """
 from __future__ import annotations
 
+import contextlib
 import math
+import threading
 
 import torch
 
@@ -490,20 +492,66 @@ def _gemm(x2: torch.Tensor, w: torch.Tensor) -> bool:
             and x2.is_cuda and N % 64 == 0 and K % 64 == 0 and w.is_contiguous())
 
 
+def _gemm_f32(x2: torch.Tensor, w: torch.Tensor) -> bool:
+    """Shapes teeny_linear_f32 takes (any M and N; K a multiple of 4)."""
+    return (_no_grad(x2, w) and x2.dtype == torch.float32 and w.dtype == torch.float32
+            and x2.is_cuda and w.shape[1] % 4 == 0 and w.is_contiguous())
+
+
+_own_gemm = threading.local()
+
+
+@contextlib.contextmanager
+def own_gemm():
+    """Within this block, products run this library's GEMMs instead of
+    hipBLASLt: bf16 products of more than 16 rows teeny_gemm_bf16, fp32
+    products teeny_gemm_f32.  That is the rule a captured graph follows by
+    itself (the linear entry points never run hipBLASLt under capture),
+    applied to eager calls so that an eager step and its graph replay run
+    the same kernels."""
+    prev = getattr(_own_gemm, "on", False)
+    _own_gemm.on = True
+    try:
+        yield
+    finally:
+        _own_gemm.on = prev
+
+
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """y = x w^T (src/layers/mod.rs:54-58; w [out, in]) through teeny_linear_bf16:
-    up to 16 rows of bf16 stream the weight (decode kernels), more rows run
-    the library's matrix-core GEMM.  fp32 (the reference's precision, used
-    by the parity tests) and products that need a gradient use torch's GEMM."""
+    """y = x w^T (src/layers/mod.rs:54-58; w [out, in]) through the library:
+    bf16 by teeny_linear_bf16 (up to 16 rows stream the weight through the
+    decode kernels, more rows run hipBLASLt, or this library's GEMM under
+    own_gemm()), fp32 (the reference's precision) by teeny_linear_f32.
+    Products that need a gradient use torch's GEMM (the library's linear
+    kernels have no backward)."""
     x2 = x.reshape(-1, x.shape[-1])
     N, K = w.shape
     if K != x2.shape[1]:
         raise ValueError(f"linear: x has {x2.shape[1]} features, w expects {K}")
+    if _gemm_f32(x2, w):
+        x2 = x2.contiguous()
+        y = torch.empty((x2.shape[0], N), dtype=x.dtype, device=x.device)
+        fn = "teeny_gemm_f32" if getattr(_own_gemm, "on", False) else "teeny_linear_f32"
+        call(fn, _p(x2), _p(w), _p(y), x2.shape[0], N, K, _stream())
+        return y.view(*x.shape[:-1], N)
     if not _gemm(x2, w):
         return torch.nn.functional.linear(x, w)
     x2 = x2.contiguous()
     y = torch.empty((x2.shape[0], N), dtype=x.dtype, device=x.device)
-    call("teeny_linear_bf16", _p(x2), _p(w), _p(y), x2.shape[0], N, K, _stream())
+    fn = ("teeny_gemm_bf16" if x2.shape[0] > 16 and getattr(_own_gemm, "on", False)
+          else "teeny_linear_bf16")
+    call(fn, _p(x2), _p(w), _p(y), x2.shape[0], N, K, _stream())
+    return y.view(*x.shape[:-1], N)
+
+
+def gemm_f32(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x w^T in fp32 through this library's own GEMM (teeny_gemm_f32)."""
+    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    N, K = w.shape
+    if K != x2.shape[1] or not _gemm_f32(x2, w):
+        raise ValueError("gemm_f32: fp32 x [.., K] and contiguous w [N, K], K a multiple of 4")
+    y = torch.empty((x2.shape[0], N), dtype=x.dtype, device=x.device)
+    call("teeny_gemm_f32", _p(x2), _p(w), _p(y), x2.shape[0], N, K, _stream())
     return y.view(*x.shape[:-1], N)
 
 

@@ -7,7 +7,7 @@ import pytest
 
 from teenyformers_amd import _lib
 
-OK, NULLP, SHAPE, UNSUP, WS, VALUE, SCRATCH = 0, -1, -2, -3, -4, -7, -8
+OK, NULLP, SHAPE, UNSUP, WS, VALUE, SCRATCH, NOT_INIT = 0, -1, -2, -3, -4, -7, -8, -9
 GRAD_F32 = 0x100
 F32, BF16 = 0, 1
 NEG_INF = float("-inf")
@@ -202,3 +202,51 @@ def test_decode_qkv_attention_validation(L):
     assert call(n=0) == SHAPE
     assert call(scale=-1.0) == VALUE
     assert call(lnb=float("nan")) == VALUE
+
+
+def test_fa2_32bit_row_offsets(L):
+    """bf16 kernels address a head's rows through 32-bit buffer offsets: a
+    head of n_ctx * D * 2 >= 2^31 bytes (Q or dO of 8.4M rows at D = 128,
+    fewer than 2^31 elements in all) is refused before any launch, on the
+    query side as on the key side."""
+    big = 8_400_000  # 8.4M * 128 * 2 B = 2.15e9 B; 8.4M * 128 = 1.08e9 elements
+    assert fwd(L, nq=big, nk=128, hq=1, hkv=1, d=128) == SHAPE
+    assert fwd(L, nq=128, nk=big, hq=1, hkv=1, d=128) == SHAPE
+    ws = 1 << 30
+    for nq, nk in ((big, 128), (128, big)):
+        rc = L.teeny_causal_flash_attn2_bwd(P, P, P, P, P, P, P, P, P, nq, nk, 0.088, 1, 1, 1,
+                                            128, BF16, P, ws, None)
+        assert rc == SHAPE, (nq, nk)
+    # fp32 kernels index elements, not byte ranges: the element bound applies
+    assert fwd(L, nq=big, nk=128, hq=1, hkv=1, d=128, dtype=F32) != SHAPE
+
+
+def test_decode_qkv_attention_32bit_cache_offsets(L):
+    """One (b, kv head) cache slab of cache_len * D * 2 >= 2^31 bytes is refused."""
+    rc = L.teeny_decode_qkv_attention_dev(P, 1, P, P, P, 1, 1, 1, 128, 8_400_000, P, 13.1,
+                                          0.088, BF16, None)
+    assert rc == SHAPE
+    rc = L.teeny_decode_qkv_attention_dev(P, 1, P, P, P, 1, 1, 1, 128, 4_000_000, P, 13.1,
+                                          0.088, BF16, None)
+    assert rc != SHAPE  # within range: fails later (no GPU here), not on the shape
+
+
+def test_noalloc_needs_init(L):
+    """The no-allocation backward loads and looks up nothing itself: without
+    a device (here) it reports the HIP error, never a launch; its
+    not-initialised code has its own text."""
+    rc = L.teeny_causal_flash_attn2_bwd_noalloc(P, P, P, P, P, P, P, P, P, 128, 128, 0.125, 1,
+                                                4, 4, 64, BF16, None)
+    assert rc in (-5, NOT_INIT)
+    assert "teeny_init" in L.teeny_strerror(NOT_INIT).decode()
+
+
+def test_linear_f32_validation(L):
+    """fp32 Linear (teeny_linear_f32 / teeny_gemm_f32): any M and N, K a
+    multiple of 4, 16-byte aligned operands."""
+    for fn in (L.teeny_linear_f32, L.teeny_gemm_f32):
+        assert fn(None, P, P, 4, 8, 8, None) == NULLP
+        assert fn(P, P, P, 0, 8, 8, None) == SHAPE
+        assert fn(P, P, P, 4, 8, 6, None) == UNSUP
+        assert fn(P + 4, P, P, 4, 8, 8, None) == VALUE
+        assert fn(P, P + 8, P, 4, 8, 8, None) == VALUE

@@ -1,7 +1,7 @@
 """GPU parity of flash-attention 2 (forward and backward) against the oracle.
 
 fp32 path: max abs <= 1e-5 against the oracle's fp32 restatement of the
-reference kernels.  bf16 path: rel-L2 <= 5e-3 and max abs <= 2e-2 against
+reference kernels, for O, LSE and the gradients alike.  bf16 path: rel-L2 <= 5e-3 and max abs <= 2e-2 against
 the fp32 oracle run on the same bf16-rounded inputs, for O and for the fp32
 gradients of the bf16 backward (TEENY_GRAD_F32); gradients stored as bf16
 get the same bar with the max-abs part scaled by the tensor's magnitude
@@ -123,8 +123,10 @@ def test_fa2_f32_fwd_bwd(cuda, shape, causal):
     dq, dk, dv = ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod, scale, causal)
     dqe, dke, dve = O.fa2_bwd(q, k, v, oe, do, le, scale, causal)
     for name, got, want in (("dq", dq, dqe), ("dk", dk, dke), ("dv", dv, dve)):
-        err = np.abs(host(got) - want).max()
-        assert err <= F32_TOL * max(1.0, np.abs(want).max()), f"{name} {err}"
+        err = float(np.abs(host(got) - want).max())
+        print(f"fa2 f32 {shape} causal={causal} {name}: max abs {err:.2e} "
+              f"(max |want| {np.abs(want).max():.2f})", flush=True)
+        assert err <= F32_TOL, f"{name} {err}"
 
 
 # ---------------------------------------------------------------------------

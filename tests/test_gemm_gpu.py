@@ -4,7 +4,9 @@ matrix-core GEMM (teeny_gemm_bf16, gemm_bf16.hip) and teeny_linear_bf16
 (hipBLASLt above 16 rows, the own GEMM as its fallback), against float64
 products of the same bf16 operands.  Bar: one bf16 rounding of the output
 (|got - want| <= 2^-8 |want|, plus 1e-6 of the output scale for the fp32
-summation order)."""
+summation order).  And the fp32 Linear (the reference's own precision):
+teeny_linear_f32 (hipBLASLt) and teeny_gemm_f32 (gemm_f32.hip) against
+float64 products within the fp32 dot-product error bound."""
 import numpy as np
 import pytest
 import torch
@@ -85,14 +87,18 @@ def test_gemm_linear_op(cuda):
     assert torch.equal(ops.linear(xs, _dev(w)), _gemm(xs, _dev(w)))
 
 
-def test_linear_under_graph_capture(cuda):
-    """A prompt-size teeny_linear_bf16 first met inside a HIP graph capture
-    runs the own GEMM (hipBLASLt's handle, plan and workspace are created
-    outside captures only); the graph replays give the eager bits each
-    time, with eager work between the replays."""
-    M, N, K = 320, 384, 512
-    x, w = _operands(M, N, K, seed=9)
+@pytest.mark.parametrize("seen_eagerly", [False, True])
+def test_linear_under_graph_capture(cuda, seen_eagerly):
+    """A prompt-size teeny_linear_bf16 inside a HIP graph capture always runs
+    the own GEMM, whether or not the shape already ran eagerly (through
+    hipBLASLt) before the capture: the graph's kernel does not depend on the
+    call history.  The replays give the own GEMM's bits each time, with eager
+    work between them."""
+    M, N, K = (320, 384, 512) if seen_eagerly else (352, 448, 576)
+    x, w = _operands(M, N, K, seed=9 + M)
     xd, wd = _dev(x), _dev(w)
+    if seen_eagerly:
+        _check(_gemm(xd, wd).float().cpu().numpy(), x, w)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -107,3 +113,98 @@ def test_linear_under_graph_capture(cuda):
         torch.cuda.synchronize()
         assert torch.equal(y, own)
         _check(_gemm(xd, wd).float().cpu().numpy(), x, w)  # eager: hipBLASLt
+
+
+# ---------------------------------------------------------------------------
+# fp32 Linear (the reference's precision): teeny_linear_f32 (hipBLASLt's fp32
+# GEMM) and teeny_gemm_f32 (the library's own), against float64 products of
+# the same operands.  Bar: the worst-case fp32 dot-product bound for any
+# summation order, |err| <= 2 K u sum_k |x_k w_k| (u = 2^-24), and rel-L2
+# within max(1e-6, u sqrt(K)) over the checked rows (a sequential fp32 sum
+# of K random-sign terms has an rms relative error near u sqrt(K / 2)).
+# ---------------------------------------------------------------------------
+F32_ENTRIES = ["teeny_gemm_f32", "teeny_linear_f32"]
+
+
+def _operands_f32(M, N, K, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((M, K)).astype(np.float32),
+            (0.02 * rng.standard_normal((N, K))).astype(np.float32))
+
+
+def _gemm_f32(x, w, entry):
+    M, K = x.shape
+    N = w.shape[0]
+    y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    _lib.call(entry, ops._p(x), ops._p(w), ops._p(y), M, N, K, ops._stream())
+    return y
+
+
+def _check_f32(got, x, w):
+    x64, w64 = x.astype(np.float64), w.astype(np.float64)
+    want = x64 @ w64.T
+    bound = 2.0 * x.shape[1] * 2.0 ** -24 * (np.abs(x64) @ np.abs(w64).T)
+    err = np.abs(got - want)
+    assert np.all(err <= bound), float((err / np.maximum(bound, 1e-30)).max())
+    rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+    assert rel <= max(1e-6, 2.0 ** -24 * np.sqrt(x.shape[1])), rel
+    return rel
+
+
+@pytest.mark.parametrize("entry", F32_ENTRIES)
+@pytest.mark.parametrize("M,N,K", [
+    (1, 8, 4), (17, 70, 36), (300, 192, 128), (129, 129, 132),  # ragged M, N, K off the tiles
+    (1000, 320, 4160), (5, 4096, 4096), (16, 128256, 512)])
+def test_linear_f32_small(cuda, M, N, K, entry):
+    x, w = _operands_f32(M, N, K, seed=M * 31 + N + K)
+    xd, wd = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+    y = _gemm_f32(xd, wd, entry)
+    _check_f32(y.cpu().numpy(), x, w)
+    assert torch.equal(y, _gemm_f32(xd, wd, entry))  # deterministic
+
+
+@pytest.mark.parametrize("entry", F32_ENTRIES)
+@pytest.mark.parametrize("M,N,K", [
+    (8192, 6144, 4096), (8192, 4096, 14336),   # Llama-3-8B prompt: qkv, down
+    (8192, 3072, 2048), (8192, 2048, 8192)])   # Llama block: qkv, down
+def test_linear_f32_llama_shapes(cuda, M, N, K, entry):
+    """fp32 prompt products at the Llama shapes; rows of the first, a middle
+    and the last 128-row tile in full width."""
+    x, w = _operands_f32(M, N, K, seed=N + K)
+    y = _gemm_f32(torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda(), entry)
+    rows = sorted({*range(0, 48), *range(M // 2 + 3, M // 2 + 35), *range(M - 48, M)})
+    rel = _check_f32(y[rows].cpu().numpy(), x[rows], w)
+    print(f"linear_f32 {entry} M{M} N{N} K{K}: rel-L2 {rel:.2e}", flush=True)
+
+
+def test_linear_f32_op(cuda):
+    """ops.linear routes fp32 products (no gradient) through teeny_linear_f32,
+    not torch; ops.gemm_f32 is the own kernel."""
+    x, w = _operands_f32(2 * 48, 320, 256, seed=5)
+    xd, wd = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+    y = ops.linear(xd.view(2, 48, 256), wd)
+    assert torch.equal(y.view(96, 320), _gemm_f32(xd, wd, "teeny_linear_f32"))
+    assert torch.equal(ops.gemm_f32(xd, wd), _gemm_f32(xd, wd, "teeny_gemm_f32"))
+    _check_f32(y.view(96, 320).cpu().numpy(), x, w)
+
+
+def test_linear_f32_under_graph_capture(cuda):
+    """Under capture teeny_linear_f32 runs the own fp32 GEMM; replays give
+    its bits each time."""
+    M, N, K = 200, 96, 160
+    x, w = _operands_f32(M, N, K, seed=12)
+    xd, wd = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+    _gemm_f32(xd, wd, "teeny_linear_f32")
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        _lib.call("teeny_linear_f32", ops._p(xd), ops._p(wd), ops._p(y), M, N, K,
+                  torch.cuda.current_stream().cuda_stream)
+    own = _gemm_f32(xd, wd, "teeny_gemm_f32")
+    for _ in range(3):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, own)

@@ -163,3 +163,20 @@ def test_generate_cli_greedy_matches_model(tmp_path, cuda):
     if 2 in want:
         want = want[:want.index(2)]
     assert buf.getvalue() == prompt + "".join(words[i] for i in want) + "\n"
+
+
+def test_config_d_ff_default_rounding():
+    """Without intermediate_size, d_ff = ceil(ceil(8 d / 3) / 64) * 64
+    (src/config.rs:146-153), the rule the reference's own config test pins
+    (tests/graph_construction.rs:55-61: d 128 -> 384, d 512 -> a multiple of
+    64), checked against exact rational arithmetic for every d to 8192."""
+    from fractions import Fraction
+    import math as _m
+
+    assert llama.LlamaConfig(d_model=128).d_ff() == 384
+    assert llama.LlamaConfig(d_model=512).d_ff() == 1408
+    assert llama.LlamaConfig().d_ff() == 10944  # the default d 4096
+    assert llama.LlamaConfig(d_model=4096, intermediate_size=14336).d_ff() == 14336
+    for d in range(1, 8193):
+        want = _m.ceil(Fraction(_m.ceil(Fraction(8 * d, 3)), 64)) * 64
+        assert llama.LlamaConfig(d_model=d).d_ff() == want, d

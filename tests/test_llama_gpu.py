@@ -111,8 +111,10 @@ def test_decode_attention_ignores_rows_past_n_keys(cuda, dtype, n_keys, L, D, Hq
     assert torch.equal(o_cap, ops.decode_attention(q, kc, vc, cap, scale))
 
 
-def _oracle_block(cfg, w, x):
-    """One LlamaBlock from the oracle's restated ops + float32 numpy GEMMs."""
+def _oracle_block(cfg, w, x, r0=0):
+    """One LlamaBlock from the oracle's restated ops + float32 numpy GEMMs:
+    the output rows r0.. of x [B, S, d] (their queries attend every key up
+    to their own position, q_offset r0)."""
     B, S, d = x.shape
     Hq, Hkv, D = cfg.n_heads, cfg.n_kv_heads(), cfg.head_dim()
     W = {k: host(v) for k, v in w.items() if k.startswith("model.layers.0.")}
@@ -120,11 +122,13 @@ def _oracle_block(cfg, w, x):
     x2d = x.reshape(B * S, d)
     n1, _ = O.rmsnorm_fwd(x2d, W[p + "input_layernorm.weight"], cfg.eps)
     qkv = (n1 @ W[p + "self_attn.qkv_proj.weight"].T).reshape(B, S, Hq + 2 * Hkv, D)
-    q = np.ascontiguousarray(qkv[:, :, :Hq].transpose(0, 2, 1, 3))
+    q = np.ascontiguousarray(qkv[:, r0:, :Hq].transpose(0, 2, 1, 3))
     k = np.ascontiguousarray(qkv[:, :, Hq:Hq + Hkv].transpose(0, 2, 1, 3))
     v = np.ascontiguousarray(qkv[:, :, Hq + Hkv:].transpose(0, 2, 1, 3))
     lnb = f32_ln(cfg.rope_base)
-    o, _ = O.fa2_fwd(O.rope(q, lnb), O.rope(k, lnb), v, cfg.softmax_scale(), causal=True)
+    o, _ = O.fa2_fwd(O.rope(q, lnb, pos0=r0), O.rope(k, lnb), v, cfg.softmax_scale(),
+                     causal=True, q_offset=r0)
+    S, x2d = S - r0, x[:, r0:].reshape(B * (S - r0), d)
     attn = O.transpose_heads(o, B, S, Hq, D, merge=True).reshape(B * S, Hq * D)
     x2 = x2d + attn @ W[p + "self_attn.o_proj.weight"].T
     n2, _ = O.rmsnorm_fwd(x2, W[p + "post_attention_layernorm.weight"], cfg.eps)
@@ -151,7 +155,10 @@ C2 = dict(d_model=2048, n_heads=32, n_layers=1, vocab_size=32, eps=1e-5, rope_ba
 def test_block_c2_shape_sampled(cuda, dtype):
     """B4 S2048 d2048, Hq32 Hkv8 D64, F8192, eps 1e-5, theta 5e5, causal.
     Causal rows 0..R-1 depend only on rows 0..R-1, so the oracle checks the
-    first 64 rows of two sequences at full width.
+    first 64 rows of two sequences at full width, and rows 1984..2047 of
+    each (their attention over all 2048 keys, the GQA-packed kernel's last
+    query blocks; the oracle forms K/V of the whole sequence and only these
+    rows' queries).
     fp32 (the reference's precision): max abs <= 1e-4 of the output scale.
     bf16: rel-L2 <= 5e-3 and max abs <= 5e-2.  The composed block runs four
     bf16 GEMMs (K = 2048 and 8192) and stores its residual stream in bf16
@@ -164,11 +171,15 @@ def test_block_c2_shape_sampled(cuda, dtype):
                     device="cuda").to(dtype)
     got = llama.block_forward(cfg, w, x)
     torch.cuda.synchronize()
-    for b in (0, 3):
-        want = _oracle_block(cfg, w, host(x[b:b + 1, :64]))
-        g = host(got[b:b + 1, :64])
+    for b, r0 in ((0, 0), (3, 0), (0, 1984), (3, 1984)):
+        if r0 == 0:
+            want = _oracle_block(cfg, w, host(x[b:b + 1, :64]))
+        else:
+            want = _oracle_block(cfg, w, host(x[b:b + 1]), r0)
+        g = host(got[b:b + 1, r0:r0 + 64])
         err = np.abs(g - want)
-        msg = f"b={b} rel-L2 {rel_l2(g, want):.3e} max abs {err.max():.3e}"
+        msg = f"b={b} rows {r0}.. rel-L2 {rel_l2(g, want):.3e} max abs {err.max():.3e}"
+        print(f"block C2 {dtype}: {msg}", flush=True)
         if dtype == torch.float32:
             assert err.max() <= 1e-4 * max(1.0, np.abs(want).max()), msg
         else:
@@ -288,15 +299,22 @@ def test_decode_qkv_attention_fused(cuda, B, Hq, Hkv, D, L):
         assert rel_l2(got, want[:, :, 0]) <= 5e-3 and np.abs(got - want[:, :, 0]).max() <= 2e-2
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_generate_graph_equals_eager(cuda, dtype):
+@pytest.mark.parametrize("dtype,batch", [(torch.float32, 3), (torch.bfloat16, 3),
+                                         (torch.bfloat16, 20), (torch.float32, 20)])
+def test_generate_graph_equals_eager(cuda, dtype, batch):
     """Greedy ids from the decode step captured in a HIP graph and replayed
-    (8 replays, eager work between them) == ids from the eager decode loop."""
+    (8 replays, eager work between them) == ids from the eager decode loop.
+    With 3 sequences the bf16 step runs the weight-streaming decode kernels;
+    with 20 (more than 16 rows) its products run the library's own GEMM both
+    eagerly and captured (a captured teeny_linear_bf16 never runs hipBLASLt),
+    and the fp32 step runs teeny_linear_f32, whose capture runs the own fp32
+    GEMM: the eager loop follows the same rule, so the bits agree."""
     cfg = llama.LlamaConfig(d_model=256, n_heads=4, n_layers=2, vocab_size=512, eps=1e-5,
                             rope_base=1e4, intermediate_size=512, n_kv_heads_=2)
     w = llama.init_weights(cfg, dtype=dtype, std=0.2, seed=23)
     model = llama.Llama(cfg, w)
-    prompt = torch.randint(0, 512, (3, 9), generator=torch.Generator(device="cuda").manual_seed(24),
+    prompt = torch.randint(0, 512, (batch, 9),
+                           generator=torch.Generator(device="cuda").manual_seed(24),
                            device="cuda")
     eager = model.generate(prompt, 10)
     graph = model.generate_graph(prompt, 10)

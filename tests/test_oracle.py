@@ -68,6 +68,26 @@ def test_rope_inverse_and_invariants():
     assert np.abs(n_x - n_y).max() < 1e-4  # rotations keep each pair's norm
 
 
+def test_rope_start_position():
+    """orc_rope_at (rows of a slice at positions pos0, pos0 + 1, ...): bit for
+    bit orc_rope of the same rows placed after pos0 zero rows, and the float64
+    closed form at positions 515..518 (a KV-cached decode step's rows)."""
+    x = rng(3).standard_normal((6, 4, 128)).astype(np.float32)
+    lnb = f32_ln(5e5)
+    for pos0 in (1, 37, 515):
+        pad = np.concatenate([np.zeros((6, pos0, 128), np.float32), x], axis=1)
+        for bwd in (False, True):
+            want = O.rope(pad, lnb, backward=bwd)[:, pos0:]
+            assert np.array_equal(O.rope(x, lnb, backward=bwd, pos0=pos0), want)
+    got = O.rope(x, lnb, pos0=515)
+    k = np.arange(64, dtype=np.float64)
+    theta = np.arange(515, 519, dtype=np.float64)[:, None] * 5e5 ** (-2 * k / 128)[None, :]
+    c, s_ = np.cos(theta), np.sin(theta)
+    xe, xo = x[..., 0::2].astype(np.float64), x[..., 1::2].astype(np.float64)
+    want = np.stack([xe * c - xo * s_, xe * s_ + xo * c], axis=-1).reshape(x.shape)
+    assert np.abs(got - want).max() < 2e-4  # fp32 theta at position ~500: |dtheta| ~ 3e-5
+
+
 def test_rope_inv_freq_rule():
     # inv = fp32(exp(fp32(k) * fp32(-2 ln b / d))), the rope.rs:88 operation order
     d, lnb = 128, f32_ln(5e5)

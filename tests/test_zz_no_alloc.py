@@ -5,7 +5,10 @@ the same size: the same kernels on the same inputs, so the gradients must be
 bit-identical.  Two calls in a row, the second on a smaller problem (the
 array keeps the first call's contents, which the second must not depend
 on), for bf16 and for bf16 with fp32 gradients; the first result is also
-held to the oracle's bf16 bar."""
+held to the oracle's bf16 bar.  The first problem's dK/dV head split (fp32
+partials in the array, then the merge kernel) runs inside the array.  And
+the entry point captured in a HIP graph: every replay equals the eager
+result, with other calls overwriting the array between replays."""
 import ctypes
 import math
 
@@ -54,8 +57,14 @@ def test_noalloc_bwd_matches_allocating_entry(cuda, grad_f32):
     scratch = L.teeny_scratch_bytes()
     assert scratch == 16 << 20
     # (B, Hq, Hkv, S, D): a GQA problem whose dK/dV head split fits in the
-    # array, then a smaller MHA one at the other head dim
-    for i, (B, Hq, Hkv, S, D) in enumerate([(2, 8, 2, 1000, 128), (1, 4, 4, 300, 64)]):
+    # array (1024 query rows, the split's lower bound: 4 partial sums of dK
+    # and dV, 4 MiB), then a smaller MHA one at the other head dim
+    cases = [(1, 8, 2, 1024, 64), (1, 4, 4, 300, 64)]
+    B, Hq, Hkv, S, D = cases[0]
+    base = L.teeny_flash_attn2_bwd_workspace_bytes(S, B, Hq, D, _lib.TEENY_BF16)
+    split = L.teeny_flash_attn2_bwd_workspace_bytes_gqa(S, S, B, Hq, Hkv, D, _lib.TEENY_BF16)
+    assert base < split <= scratch, (base, split)
+    for i, (B, Hq, Hkv, S, D) in enumerate(cases):
         print(f"noalloc call {i}: B{B} Hq{Hq} Hkv{Hkv} S{S} D{D} grad_f32={grad_f32}", flush=True)
         q, k, v, do = _inputs(B, Hq, Hkv, S, D, seed=90 + i)
         scale = 1.0 / math.sqrt(D)
@@ -76,3 +85,41 @@ def test_noalloc_bwd_matches_allocating_entry(cuda, grad_f32):
                 rel = float(np.linalg.norm(g - w) / np.linalg.norm(w))
                 assert rel <= 5e-3 and err <= 2e-2 * max(1.0, float(np.abs(w).max()) / 4), \
                     f"{name}: max abs {err:.3e} rel-L2 {rel:.3e}"
+
+
+def test_noalloc_bwd_under_graph_capture(cuda):
+    """The entry point recorded in a HIP graph (it loads and allocates
+    nothing, and clears nothing with a memset node): three replays, each
+    after eager calls of the same entry point on another problem have
+    overwritten the shared array, give the eager gradients bit for bit."""
+    B, Hq, Hkv, S, D = 1, 8, 2, 1024, 64  # with the dK/dV head split in the array
+    q, k, v, do = _inputs(B, Hq, Hkv, S, D, seed=95)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = ops.flash_attn2_fwd(q, k, v, scale, True)
+    want = _noalloc(q, k, v, o, lse, do, scale, False)
+    q2, k2, v2, do2 = _inputs(1, 4, 4, 700, 128, seed=96)
+    o2, lse2 = ops.flash_attn2_fwd(q2, k2, v2, 1.0 / math.sqrt(128), True)
+    torch.cuda.synchronize()
+
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = _lib.lib().teeny_causal_flash_attn2_bwd_noalloc(
+            _p(q), _p(k), _p(v), _p(o), _p(do), _p(lse), _p(dq), _p(dk), _p(dv), S, S, scale, B,
+            Hq, Hkv, D, _lib.TEENY_BF16, stream)
+    assert rc == 0, _lib.strerror(rc)
+    for r in range(3):
+        # another problem through the same array, eagerly, between replays
+        _noalloc(q2, k2, v2, o2, lse2, do2, 1.0 / math.sqrt(128), r % 2 == 1)
+        for t in (dq, dk, dv):
+            t.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        print(f"noalloc graph replay {r}", flush=True)
+        for name, got, w in zip(("dQ", "dK", "dV"), (dq, dk, dv), want):
+            assert torch.equal(got, w), f"replay {r}: {name}"
