@@ -441,6 +441,9 @@ def bench_llama_8b(torch):
         cache_holder["c"], cache_holder["l"] = model.prefill(ids, Sp + n_new)
 
     prefill_ms = _time(torch, prefill, 3)
+    # the reference's Llama::forward (src/llama.rs:65-81) computes every
+    # position's logits; the generation prefill above only the last one's
+    fwd_all_ms = _time(torch, lambda: model.forward(ids), 3)
     cache, logits = cache_holder["c"], cache_holder["l"]
     nxt = ops.argmax_rows(logits).view(-1, 1)
     # decode: the step captured once in a HIP graph (its first run is step 1),
@@ -453,12 +456,17 @@ def bench_llama_8b(torch):
     torch.cuda.synchronize()
     decode_ms = (time.perf_counter() - t0) * 1e3 / (n_new - 1)
     f = llama.prefill_flops(cfg, Bq, Sp)
+    f_all = llama.prefill_flops(cfg, Bq, Sp, last_logits_only=False)
     wbytes = sum(t.numel() * t.element_size() for t in w.values())
     del w, model, cache, dg
     return {"prefill_ms": round(prefill_ms, 2),
             "prefill_tokens_per_s": round(Bq * Sp / prefill_ms * 1e3, 1),
             "prefill_tflops": round(f / prefill_ms / 1e9, 1),
             "prefill_pct_peak": round(f / prefill_ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+            "prefill_logits": "last prompt position only (what generation needs)",
+            "forward_all_logits_ms": round(fwd_all_ms, 2),
+            "forward_all_logits_tokens_per_s": round(Bq * Sp / fwd_all_ms * 1e3, 1),
+            "forward_all_logits_tflops": round(f_all / fwd_all_ms / 1e9, 1),
             "decode_ms_per_step": round(decode_ms, 3),
             "decode_tokens_per_s": round(Bq / decode_ms * 1e3, 1),
             "decode_weight_gbs": round(wbytes / decode_ms / 1e6, 1),
