@@ -371,6 +371,30 @@ int teeny_gemm_f32(const void* x, const void* w, void* y, int M, int N, int K,
 int teeny_linear_partials_count(int K, int k_split);
 int teeny_linear_partials_bf16(const void* x, const void* w, float* parts, int M, int N, int K,
                                int k_split, hipStream_t stream);
+
+/* The streaming layout of a bf16 weight W [N, K] (row-major, the HF [out,
+ * in] layout of src/loader.rs:19-27) for the decode-step kernels: a copy
+ * w_s of N*K bf16 in the order their wavefronts load it,
+ *   w_s[nb][ks][q][g][r][e] = W[16 nb + r][128 ks + 32 g + 8 q + e]
+ * (nb < N/16, ks < K/128, q, g < 4, r < 16, e < 8), so that each load
+ * instruction reads one contiguous KiB.  N % 16 == 0 and K % 128 == 0
+ * (TEENY_ERR_UNSUPPORTED otherwise); w and w_s must not overlap
+ * (TEENY_ERR_INVALID_VALUE).  Done once per weight, at load time.
+ * teeny_linear_sl_bf16, teeny_linear_swiglu_sl_bf16 (w_s: the layout of the
+ * fused [2F, K] gate_up weight) and teeny_linear_partials_sl_bf16 are
+ * teeny_linear_bf16, teeny_linear_swiglu_bf16 and teeny_linear_partials_bf16
+ * at up to 16 rows (M <= 16, N % 128 == 0 or F % 64 == 0, K % 128 == 0;
+ * TEENY_ERR_UNSUPPORTED otherwise) reading W from w_s: the same products in
+ * the same order, bit-identical outputs, in 3-9 % less time on weights that
+ * stream from HBM.  No reference counterpart: a layout for this library's
+ * decode kernels, costing one more copy of the weights they read. */
+int teeny_linear_stream_layout_bf16(const void* w, void* w_s, int N, int K, hipStream_t stream);
+int teeny_linear_sl_bf16(const void* x, const void* w_s, void* y, int M, int N, int K,
+                         hipStream_t stream);
+int teeny_linear_swiglu_sl_bf16(const void* x, const void* w_s, void* y, int M, int F, int K,
+                                hipStream_t stream);
+int teeny_linear_partials_sl_bf16(const void* x, const void* w_s, float* parts, int M, int N,
+                                  int K, int k_split, hipStream_t stream);
 int teeny_fused_add_rmsnorm_partials_fwd(const float* parts, int n_parts, const void* residual,
                                          void* y, void* h, float* rstd, const void* weight,
                                          int M, int N, float eps, int dtype,

@@ -80,6 +80,10 @@ _SIGNATURES = {
     "teeny_gemm_f32": ([_p, _p, _p, _i, _i, _i, _p], _i),
     "teeny_linear_partials_count": ([_i, _i], _i),
     "teeny_linear_partials_bf16": ([_p, _p, _p, _i, _i, _i, _i, _p], _i),
+    "teeny_linear_stream_layout_bf16": ([_p, _p, _i, _i, _p], _i),
+    "teeny_linear_sl_bf16": ([_p, _p, _p, _i, _i, _i, _p], _i),
+    "teeny_linear_swiglu_sl_bf16": ([_p, _p, _p, _i, _i, _i, _p], _i),
+    "teeny_linear_partials_sl_bf16": ([_p, _p, _p, _i, _i, _i, _i, _p], _i),
     "teeny_fused_add_rmsnorm_partials_fwd": ([_p, _i, _p, _p, _p, _p, _p, _i, _i, _f, _i, _p], _i),
     "teeny_qkv_rope_split_partials_dev": ([_p, _i, _p, _p, _p, _i, _i, _p, _i, _i, _i, _i, _f,
                                            _i, _p], _i),

@@ -1134,6 +1134,54 @@ int teeny_linear_partials_bf16(const void* x, const void* w, float* parts, int M
   return launch("teeny_linear_sk_part_bf16", dim3(N / 128, n), dim3(512), 0, stream, args);
 }
 
+// The streaming layout of a decode weight (linear_bf16.hip): a copy of W in
+// the order the decode kernels' wavefronts load it, 16-byte pieces, 256
+// threads per workgroup.
+int teeny_linear_stream_layout_bf16(const void* w, void* w_s, int N, int K, hipStream_t stream) {
+  if (!w || !w_s) return TEENY_ERR_NULL_POINTER;
+  if (N <= 0 || K <= 0 || (long)N * K >= kMaxElems * 2) return TEENY_ERR_INVALID_SHAPE;
+  if (N % 16 != 0 || K % 128 != 0) return TEENY_ERR_UNSUPPORTED;
+  const char *a = (const char*)w, *b = (const char*)w_s;
+  const long bytes = (long)N * K * 2;
+  if (a < b + bytes && b < a + bytes) return TEENY_ERR_INVALID_VALUE;  // in place or overlapping
+  long n_pieces = (long)N * K / 8;
+  void* args[] = {&w, &w_s, &N, &K, &n_pieces};
+  return launch("teeny_linear_stream_layout_bf16", dim3((unsigned)((n_pieces + 255) / 256)),
+                dim3(256), 0, stream, args);
+}
+
+// teeny_linear_bf16, teeny_linear_swiglu_bf16 and teeny_linear_partials_bf16
+// at up to 16 rows with the weight in the streaming layout: the same kernels
+// reading the layout, the same outputs.
+int teeny_linear_sl_bf16(const void* x, const void* w_s, void* y, int M, int N, int K,
+                         hipStream_t stream) {
+  int rc = linear_sk_check(x, w_s, y, M, N, K, N, 128);
+  if (rc) return rc;
+  void* args[] = {&x, &w_s, &y, &M, &N, &K};
+  return launch("teeny_linear_sl_bf16", dim3(N / 128), dim3(512), 0, stream, args);
+}
+
+int teeny_linear_swiglu_sl_bf16(const void* x, const void* w_s, void* y, int M, int F, int K,
+                                hipStream_t stream) {
+  int rc = linear_sk_check(x, w_s, y, M, F, K, 2L * F, 64);
+  if (rc) return rc;
+  void* args[] = {&x, &w_s, &y, &M, &F, &K};
+  return launch("teeny_linear_sl_swiglu_bf16", dim3(F / 64), dim3(512), 0, stream, args);
+}
+
+int teeny_linear_partials_sl_bf16(const void* x, const void* w_s, float* parts, int M, int N,
+                                  int K, int k_split, hipStream_t stream) {
+  int rc = linear_sk_check(x, w_s, parts, M, N, K, N, 128);
+  if (rc) return rc;
+  if (k_split <= 0) return TEENY_ERR_INVALID_VALUE;
+  if (k_split >= K) k_split = K;
+  else if (k_split % 128 != 0) return TEENY_ERR_INVALID_VALUE;  // whole 128-wide K steps
+  const int n = teeny_linear_partials_count(K, k_split);
+  if (n > 65535) return TEENY_ERR_INVALID_SHAPE;
+  void* args[] = {&x, &w_s, &parts, &M, &N, &K, &k_split};
+  return launch("teeny_linear_sl_part_bf16", dim3(N / 128, n), dim3(512), 0, stream, args);
+}
+
 int teeny_token_embed_fwd(const void* ids, const void* weight, void* out, int seq_len,
                           int d_model, int vocab_size, int ids_dtype, int dtype,
                           hipStream_t stream) {

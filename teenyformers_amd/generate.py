@@ -92,6 +92,8 @@ def generate_text(args) -> int:
     print(args.prompt, end="", flush=True)
     prompt = torch.tensor([ids], dtype=torch.int64, device="cuda")
     cache, logits = model.prefill(prompt, len(ids) + args.max_new_tokens)
+    if not args.no_stream_layout:
+        model.stream_layout()
     rng = XorShift(args.seed)
     dg = None
     for step in range(args.max_new_tokens):
@@ -131,6 +133,8 @@ def bench_preset(args) -> int:
     torch.cuda.synchronize()
     prefill_ms = (time.perf_counter() - t0) * 1e3
     print(f"prefill {prefill_ms:.1f} ms", file=sys.stderr, flush=True)
+    if not args.no_stream_layout:
+        model.stream_layout()
     dg = llama.DecodeGraph(model, cache, ops.argmax_rows(logits).view(-1, 1))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -156,6 +160,8 @@ def main(argv=None) -> int:
     ap.add_argument("--preset", choices=sorted(PRESETS), help="random weights, timing only")
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--prompt-len", type=int, default=512)
+    ap.add_argument("--no-stream-layout", action="store_true",
+                    help="decode from the row-major weights (saves one copy of them)")
     args = ap.parse_args(argv)
     if args.max_new_tokens < 1:
         ap.error("--max-new-tokens must be at least 1")

@@ -178,6 +178,31 @@ class Llama:
         self.cfg = cfg
         self.w = weights
         self.decode_ws = None
+        self.sw = {}  # streaming-layout copies of the decode weights (stream_layout)
+
+    def stream_layout(self) -> "Llama":
+        """Give the weights that one-token steps stream (each layer's qkv, o,
+        gate_up and down projections and the tied lm_head) a streaming-layout
+        copy (ops.StreamWeight): the decode linears then read 1 KiB per load
+        instruction, with the same outputs; prompt-sized products keep the
+        row-major weights.  Costs one more copy of those weights.  bf16 only;
+        weights whose shape the layout does not take are left as they are."""
+        names = ["model.embed_tokens.weight"]
+        for i in range(self.cfg.n_layers):
+            p = f"model.layers.{i}."
+            names += [p + "self_attn.qkv_proj.weight", p + "self_attn.o_proj.weight",
+                      p + "mlp.gate_up_proj.weight", p + "mlp.down_proj.weight"]
+        for n in names:
+            w = self.w[n]
+            if (n not in self.sw and w.dtype == torch.bfloat16 and w.is_cuda
+                    and w.shape[0] % 16 == 0 and w.shape[1] % 128 == 0):
+                self.sw[n] = ops.StreamWeight(w)
+        return self
+
+    def _lw(self, name: str):
+        """The weight of a linear layer: its StreamWeight if stream_layout()
+        made one, else the tensor."""
+        return self.sw.get(name, self.w[name])
 
     # -- one block (src/layers/llama_block.rs:55-65) -------------------------
     def _attention(self, i: int, n1: torch.Tensor, cache: KVCache, pos0) -> torch.Tensor:
@@ -188,13 +213,13 @@ class Llama:
         Hq, Hkv, D = cfg.n_heads, cfg.n_kv_heads(), cfg.head_dim()
         p = f"model.layers.{i}.self_attn."
         # [B, S, (Hq+2Hkv) D]; K-split fp32 slabs at decode sizes
-        qkv = ops.linear_split(n1, w[p + "qkv_proj.weight"])
+        qkv = ops.linear_split(n1, self._lw(p + "qkv_proj.weight"))
         scale = cfg.softmax_scale()
         if isinstance(pos0, torch.Tensor) and self._fused_decode(qkv, cache):
             # one launch: QKV split, RoPE, cache write and attention
             o = ops.decode_qkv_attention(qkv, cache.k[i], cache.v[i], pos0, Hq, Hkv,
                                          cfg.rope_base, scale)
-            return ops.linear_split(o.view(B, 1, Hq * D), w[p + "o_proj.weight"])
+            return ops.linear_split(o.view(B, 1, Hq * D), self._lw(p + "o_proj.weight"))
         q = torch.empty((B, Hq, S, D), dtype=n1.dtype, device=n1.device)
         ops.qkv_rope_split(qkv, q, cache.k[i], cache.v[i], pos0, Hq, Hkv, cfg.rope_base)
         if isinstance(pos0, torch.Tensor):  # graph decode: the position is on the device
@@ -214,7 +239,7 @@ class Llama:
             o, _ = ops.flash_attn2_fwd(q, cache.k[i], cache.v[i], scale, causal=True)
         # one position: [B, Hq, 1, D] is already the merged [B, 1, Hq D] layout
         att = o.view(B, S, Hq * D) if S == 1 else ops.merge_heads(o)
-        return ops.linear_split(att, w[p + "o_proj.weight"])
+        return ops.linear_split(att, self._lw(p + "o_proj.weight"))
 
     def _fused_decode(self, qkv, cache: KVCache) -> bool:
         """Whether a one-token step runs teeny_decode_qkv_attention_dev: bf16
@@ -236,8 +261,8 @@ class Llama:
     def _ffn(self, i: int, n2: torch.Tensor) -> torch.Tensor:
         """src/layers/ffn.rs:47-56."""
         p = f"model.layers.{i}.mlp."
-        f = ops.linear_swiglu(n2, self.w[p + "gate_up_proj.weight"])
-        return ops.linear_split(f, self.w[p + "down_proj.weight"])
+        f = ops.linear_swiglu(n2, self._lw(p + "gate_up_proj.weight"))
+        return ops.linear_split(f, self._lw(p + "down_proj.weight"))
 
     def hidden(self, ids: torch.Tensor, cache: KVCache, pos0, trace: list | None = None
                ) -> torch.Tensor:
@@ -276,7 +301,7 @@ class Llama:
 
     def logits(self, h: torch.Tensor) -> torch.Tensor:
         """Tied lm_head (src/layers/embedding.rs:159-167): h @ E^T."""
-        return ops.linear(h, self.w["model.embed_tokens.weight"])
+        return ops.linear(h, self._lw("model.embed_tokens.weight"))
 
     def forward(self, ids: torch.Tensor) -> torch.Tensor:
         """All-position logits [B, S, vocab] (src/llama.rs:65-81)."""

@@ -517,17 +517,51 @@ def own_gemm():
         _own_gemm.on = prev
 
 
-def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+class StreamWeight:
+    """A bf16 weight W [N, K] with its streaming-layout copy
+    (teeny_linear_stream_layout_bf16: the order in which the decode-step
+    kernels load it, one contiguous KiB per load instruction).  linear,
+    linear_swiglu and linear_split take it in place of the tensor: products
+    of up to 16 rows read the copy (teeny_linear_*sl_bf16, the same outputs),
+    other products the row-major W.  Costs one more copy of W."""
+
+    def __init__(self, w: torch.Tensor):
+        if w.dim() != 2 or w.dtype != torch.bfloat16 or not w.is_cuda or not w.is_contiguous():
+            raise ValueError("StreamWeight: a contiguous bf16 [N, K] device tensor")
+        N, K = w.shape
+        if N % 16 or K % 128:
+            raise ValueError("StreamWeight: N must be a multiple of 16 and K of 128")
+        self.w = w
+        self.s = torch.empty_like(w)
+        call("teeny_linear_stream_layout_bf16", _p(w), _p(self.s), N, K, _stream())
+
+    @property
+    def shape(self):
+        return self.w.shape
+
+
+def _row_major(w):
+    return w.w if isinstance(w, StreamWeight) else w
+
+
+def linear(x: torch.Tensor, w) -> torch.Tensor:
     """y = x w^T (src/layers/mod.rs:54-58; w [out, in]) through the library:
     bf16 by teeny_linear_bf16 (up to 16 rows stream the weight through the
     decode kernels, more rows run hipBLASLt, or this library's GEMM under
     own_gemm()), fp32 (the reference's precision) by teeny_linear_f32.
     Products that need a gradient use torch's GEMM (the library's linear
-    kernels have no backward)."""
+    kernels have no backward).  w may be a StreamWeight."""
     x2 = x.reshape(-1, x.shape[-1])
     N, K = w.shape
     if K != x2.shape[1]:
         raise ValueError(f"linear: x has {x2.shape[1]} features, w expects {K}")
+    if isinstance(w, StreamWeight):
+        if _skinny(x2, w.w, N):
+            x2 = x2.contiguous()
+            y = torch.empty((x2.shape[0], N), dtype=x.dtype, device=x.device)
+            call("teeny_linear_sl_bf16", _p(x2), _p(w.s), _p(y), x2.shape[0], N, K, _stream())
+            return y.view(*x.shape[:-1], N)
+        w = w.w
     if _gemm_f32(x2, w):
         x2 = x2.contiguous()
         y = torch.empty((x2.shape[0], N), dtype=x.dtype, device=x.device)
@@ -568,23 +602,29 @@ def gemm_own(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return y.view(*x.shape[:-1], N)
 
 
-def linear_swiglu(x: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
+def linear_swiglu(x: torch.Tensor, w_gate_up) -> torch.Tensor:
     """swiglu(x w_gate_up^T) (src/layers/ffn.rs:47-56).  Up to 16 bf16 rows
     without gradients: one launch of teeny_linear_swiglu_bf16 (the decode
     kernel with the SwiGLU fused).  More rows: the linear entry point
     (hipBLASLt) and then the SwiGLU kernel, measured faster than the own GEMM
     with the SwiGLU epilogue (1.40 against 1.52 ms at 8192 x 28672 x 4096);
-    other cases: the GEMM followed by the SwiGLU kernel."""
+    other cases: the GEMM followed by the SwiGLU kernel.  w_gate_up may be a
+    StreamWeight."""
     x2 = x.reshape(-1, x.shape[-1])
     N2, K = w_gate_up.shape
     if K != x2.shape[1] or N2 % 2:
         raise ValueError("linear_swiglu: weight must be [2F, in] with in = x's features")
     F = N2 // 2
-    if not _gemm(x2, w_gate_up) or not _skinny(x2, w_gate_up, F, row_tile=64):
-        return swiglu(linear(x, w_gate_up))
+    w = _row_major(w_gate_up)
+    if not _gemm(x2, w) or not _skinny(x2, w, F, row_tile=64):
+        return swiglu(linear(x, w))
     x2 = x2.contiguous()
     y = torch.empty((x2.shape[0], F), dtype=x.dtype, device=x.device)
-    call("teeny_linear_swiglu_bf16", _p(x2), _p(w_gate_up), _p(y), x2.shape[0], F, K, _stream())
+    if isinstance(w_gate_up, StreamWeight):
+        call("teeny_linear_swiglu_sl_bf16", _p(x2), _p(w_gate_up.s), _p(y), x2.shape[0], F, K,
+             _stream())
+    else:
+        call("teeny_linear_swiglu_bf16", _p(x2), _p(w), _p(y), x2.shape[0], F, K, _stream())
     return y.view(*x.shape[:-1], F)
 
 
@@ -616,20 +656,25 @@ def _k_split(K: int, N: int) -> int:
     return -(-steps // best) * 128
 
 
-def linear_split(x: torch.Tensor, w: torch.Tensor, k_split: int | None = None):
+def linear_split(x: torch.Tensor, w, k_split: int | None = None):
     """x w^T as Partials where the decode kernels take the shape (up to 16
     bf16 rows), else the GEMM's tensor.  k_split (a multiple of 128) sets K
-    per slab; by default it is chosen to spread the work over the CUs."""
+    per slab; by default it is chosen to spread the work over the CUs.  w may
+    be a StreamWeight."""
     x2 = x.reshape(-1, x.shape[-1])
     N, K = w.shape
     if K != x2.shape[1]:
         raise ValueError(f"linear: x has {x2.shape[1]} features, w expects {K}")
-    if not _skinny(x2, w, N):
-        return linear(x, w)
+    if not _skinny(x2, _row_major(w), N):
+        return linear(x, _row_major(w))
     x2 = x2.contiguous()
     ks = _k_split(K, N) if k_split is None else k_split
     n = _lib.lib().teeny_linear_partials_count(K, ks)
     slabs = torch.empty((n, x2.shape[0], N), dtype=torch.float32, device=x.device)
-    call("teeny_linear_partials_bf16", _p(x2), _p(w), _p(slabs), x2.shape[0], N, K, ks,
-         _stream())
+    if isinstance(w, StreamWeight):
+        call("teeny_linear_partials_sl_bf16", _p(x2), _p(w.s), _p(slabs), x2.shape[0], N, K, ks,
+             _stream())
+    else:
+        call("teeny_linear_partials_bf16", _p(x2), _p(w), _p(slabs), x2.shape[0], N, K, ks,
+             _stream())
     return Partials(slabs, (*x.shape[:-1], N), x.dtype)

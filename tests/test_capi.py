@@ -250,3 +250,26 @@ def test_linear_f32_validation(L):
         assert fn(P, P, P, 4, 8, 6, None) == UNSUP
         assert fn(P + 4, P, P, 4, 8, 8, None) == VALUE
         assert fn(P, P + 8, P, 4, 8, 8, None) == VALUE
+
+
+def test_stream_layout_validation(L):
+    """The streaming layout (N % 16, K % 128, no overlap) and the linears
+    that read it (the decode kernels' shapes only: M <= 16, N % 128 or
+    F % 64, K % 128)."""
+    Q = P + (1 << 30)  # a second buffer far from P
+    assert L.teeny_linear_stream_layout_bf16(None, Q, 16, 128, None) == NULLP
+    assert L.teeny_linear_stream_layout_bf16(P, Q, 0, 128, None) == SHAPE
+    assert L.teeny_linear_stream_layout_bf16(P, Q, 24, 128, None) == UNSUP
+    assert L.teeny_linear_stream_layout_bf16(P, Q, 16, 96, None) == UNSUP
+    assert L.teeny_linear_stream_layout_bf16(P, P, 16, 128, None) == VALUE  # in place
+    assert L.teeny_linear_stream_layout_bf16(P, P + 2 * 16 * 128 - 2, 16, 128, None) == VALUE
+    assert L.teeny_linear_stream_layout_bf16(P, Q, 1 << 16, 1 << 16, None) == SHAPE
+    assert L.teeny_linear_sl_bf16(None, P, P, 4, 128, 128, None) == NULLP
+    assert L.teeny_linear_sl_bf16(P, P, P, 17, 128, 128, None) == UNSUP  # prompt sizes: row-major
+    assert L.teeny_linear_sl_bf16(P, P, P, 4, 96, 128, None) == UNSUP
+    assert L.teeny_linear_sl_bf16(P, P, P, 4, 128, 192, None) == UNSUP
+    assert L.teeny_linear_swiglu_sl_bf16(P, P, P, 4, 96, 128, None) == UNSUP
+    assert L.teeny_linear_swiglu_sl_bf16(P, P, P, 0, 64, 128, None) == SHAPE
+    assert L.teeny_linear_partials_sl_bf16(P, P, P, 4, 128, 4096, 1000, None) == VALUE
+    assert L.teeny_linear_partials_sl_bf16(P, P, P, 4, 128, 4096, 0, None) == VALUE
+    assert L.teeny_linear_partials_sl_bf16(P, None, P, 4, 128, 4096, 512, None) == NULLP

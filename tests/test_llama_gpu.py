@@ -321,8 +321,58 @@ def test_generate_graph_equals_eager(cuda, dtype, batch):
     assert torch.equal(eager, graph), (eager, graph)
 
 
+def test_generate_stream_layout_equals_row_major(cuda):
+    """Greedy ids of the graph-replayed decode with the weights in the
+    streaming layout (ops.StreamWeight) == the eager decode from the
+    row-major weights: the layout changes only the order of the loads."""
+    cfg = llama.LlamaConfig(d_model=256, n_heads=4, n_layers=2, vocab_size=512, eps=1e-5,
+                            rope_base=1e4, intermediate_size=512, n_kv_heads_=2)
+    w = llama.init_weights(cfg, dtype=torch.bfloat16, std=0.2, seed=29)
+    prompt = torch.randint(0, 512, (5, 9), generator=torch.Generator(device="cuda").manual_seed(30),
+                           device="cuda")
+    eager = llama.Llama(cfg, w).generate(prompt, 10)
+    model = llama.Llama(cfg, w).stream_layout()
+    assert len(model.sw) == 1 + 4 * cfg.n_layers
+    graph = model.generate_graph(prompt, 10)
+    assert torch.equal(eager, graph), (eager, graph)
+
+
 def _bf16_dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).to("cuda", torch.bfloat16)
+
+
+@pytest.mark.parametrize("N,K", [(16, 128), (48, 640), (4096, 4224)])
+def test_stream_layout(cuda, N, K):
+    """teeny_linear_stream_layout_bf16 against its definition:
+    w_s[nb][ks][q][g][r][e] = W[16 nb + r][128 ks + 32 g + 8 q + e]."""
+    w = torch.randn(N, K, device="cuda").to(torch.bfloat16)
+    got = ops.StreamWeight(w).s.view(torch.int16).cpu().numpy()
+    want = (w.view(torch.int16).cpu().numpy().reshape(N // 16, 16, K // 128, 4, 4, 8)
+            .transpose(0, 2, 4, 3, 1, 5).reshape(N, K))
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("M,N,K,k_split", [
+    (1, 128, 128, None), (5, 256, 640, None),    # partial 512-wide chunks
+    (16, 4096, 4096, None), (16, 6144, 4096, 896), (16, 4096, 14336, 1792),
+    (7, 128, 4224, 384), (16, 1024, 4096, 4096)])
+def test_linear_stream_layout_bit_exact(cuda, M, N, K, k_split):
+    """The decode linears reading the streaming layout give the same bits
+    as the row-major kernels: the product (teeny_linear_sl_bf16), the
+    K-split slabs (teeny_linear_partials_sl_bf16) and, on [N, K] read as a
+    fused [2F, K] gate_up weight, SwiGLU (teeny_linear_swiglu_sl_bf16)."""
+    g = torch.Generator(device="cuda").manual_seed(M * 131 + N + K)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    w = (0.02 * torch.randn(N, K, device="cuda", generator=g)).to(torch.bfloat16)
+    sw = ops.StreamWeight(w)
+    assert torch.equal(ops.linear(x, sw), ops.linear(x, w))
+    p_sl, p_rm = ops.linear_split(x, sw, k_split), ops.linear_split(x, w, k_split)
+    assert p_sl.n == p_rm.n and torch.equal(p_sl.slabs, p_rm.slabs)
+    if N % 128 == 0:  # F = N / 2, a multiple of 64
+        assert torch.equal(ops.linear_swiglu(x, sw), ops.linear_swiglu(x, w))
+    # more than 16 rows: the row-major weight (the GEMM), same as without it
+    x20 = torch.randn(20, K, device="cuda", generator=g).to(torch.bfloat16)
+    assert torch.equal(ops.linear(x20, sw), ops.linear(x20, w))
 
 
 @pytest.mark.parametrize("M,N,K", [
