@@ -183,7 +183,15 @@ def main() -> int:
     }
 
     if not args.no_power:
-        out["detail"]["power"] = sample_power(torch, step, seconds=2.0)
+        pw = sample_power(torch, step, seconds=2.0)
+        if pw is not None:
+            # dense bf16 peak at the clock the board held: CUs x 4 SIMDs x 1024
+            # FLOP per clock (one 32x32x16 MFMA per 32 clocks per SIMD)
+            cus = torch.cuda.get_device_properties(0).multi_processor_count
+            at_clk = cus * 4096 * pw["engine_clock_mhz"] * 1e6 / 1e12
+            pw["peak_bf16_tflops_at_clock"] = round(at_clk, 1)
+            pw["step_pct_of_clock_peak"] = round(out["value"] / at_clk, 4)
+        out["detail"]["power"] = pw
     if not args.no_extra:
         del q, k, v, do, o, lse, dq, dk, dv, ws
         torch.cuda.empty_cache()
