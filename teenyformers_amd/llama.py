@@ -186,7 +186,9 @@ class Llama:
         copy (ops.StreamWeight): the decode linears then read 1 KiB per load
         instruction, with the same outputs; prompt-sized products keep the
         row-major weights.  Costs one more copy of those weights.  bf16 only;
-        weights whose shape the layout does not take are left as they are."""
+        weights whose shape the layout does not take are left as they are.
+        The copies are made once: after changing the weights in place, clear
+        self.sw and call this again."""
         names = ["model.embed_tokens.weight"]
         for i in range(self.cfg.n_layers):
             p = f"model.layers.{i}."

@@ -523,7 +523,8 @@ class StreamWeight:
     kernels load it, one contiguous KiB per load instruction).  linear,
     linear_swiglu and linear_split take it in place of the tensor: products
     of up to 16 rows read the copy (teeny_linear_*sl_bf16, the same outputs),
-    other products the row-major W.  Costs one more copy of W."""
+    other products the row-major W.  Costs one more copy of W.  The copy is
+    made once, here: after an in-place change of W, make a new StreamWeight."""
 
     def __init__(self, w: torch.Tensor):
         if w.dim() != 2 or w.dtype != torch.bfloat16 or not w.is_cuda or not w.is_contiguous():
