@@ -273,3 +273,28 @@ def test_stream_layout_validation(L):
     assert L.teeny_linear_partials_sl_bf16(P, P, P, 4, 128, 4096, 1000, None) == VALUE
     assert L.teeny_linear_partials_sl_bf16(P, P, P, 4, 128, 4096, 0, None) == VALUE
     assert L.teeny_linear_partials_sl_bf16(P, None, P, 4, 128, 4096, 512, None) == NULLP
+
+
+def test_header_is_c(tmp_path):
+    """include/teeny_hip.h is a C header: a C99 program that includes it
+    compiles without warnings, links against libteeny_hip.so and calls it
+    (what a cgo / bindgen / ctypes consumer relies on)."""
+    import os
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    libdir = os.path.join(root, "teenyformers_amd")
+    src = tmp_path / "use_header.c"
+    src.write_text('#include "teeny_hip.h"\n'
+                   "int main(void) { return teeny_abi_version() == 1 ? 0 : 1; }\n")
+    exe = tmp_path / "use_header"
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__",
+                    "-I" + os.path.join(root, "include"), "-I" + os.path.join(rocm, "include"),
+                    str(src), "-L" + libdir, "-lteeny_hip", "-Wl,-rpath," + libdir,
+                    "-o", str(exe)], check=True)
+    assert subprocess.run([str(exe)]).returncode == 0
