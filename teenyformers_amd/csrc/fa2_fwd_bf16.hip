@@ -8,13 +8,16 @@
 // fp32 online softmax.
 //
 // Tiling (one workgroup = 4 wavefronts = 128 query rows of one (b, h); two
-// workgroups per CU, so the two waves on each SIMD run independently and
-// cover each other's MFMA / VALU phases.  Long GQA sequences take the _w8
-// form: 8 wavefronts = 256 rows share each K/V tile, one workgroup per CU,
-// half the L2 -> LDS traffic per product):
+// or three workgroups per CU, so the waves on each SIMD run independently
+// and cover each other's MFMA / VALU phases: the causal D = 128 forms take
+// 32-key tiles, whose registers (168) and LDS (40 KiB) let three workgroups
+// share a CU, the others 64-key tiles (three per CU at D = 64, two at
+// D = 128).  Long GQA sequences take the _w8 form: 8 wavefronts = 256 rows
+// share each K/V tile, one workgroup per CU, half the L2 -> LDS traffic per
+// product):
 //   * each wave owns 32 query rows; its Q rows live in registers as the
 //     B operand of v_mfma_f32_32x32x16_bf16;
-//   * K/V advance in tiles of 64 keys that buffer_load ... lds streams into
+//   * K/V advance in tiles of 64 (or 32) keys that buffer_load ... lds streams into
 //     LDS one tile ahead (K: 2 buffers, V: 3, since the PV product of a tile
 //     runs one iteration late); K is stored SWZ_ROW and read row-wise as the
 //     A operand of S^T = K Q^T, V is stored SWZ_DUAL and read with the LDS
@@ -47,25 +50,29 @@
 
 namespace {
 
-constexpr int BN = 64;   // keys per iteration
+constexpr int SUBN = 32;  // keys per subtile: one S^T accumulator of 32 keys x 32 rows
 constexpr int KBUF = 2;  // K tiles in flight: read by QK(i), loading i+1
 constexpr int VBUF = 3;  // V tiles: read by PV(i-1), waiting (i), loading (i+1)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kPmax = 2147483648.0f;  // 2^31: a tile's partial row sums stay below
 
-template <int D>
+template <int D, int NSUB>
 struct __attribute__((aligned(16))) FwdSmem {
-  char k[KBUF][BN * D * 2];
-  char v[VBUF][BN * D * 2];
+  char k[KBUF][SUBN * NSUB * D * 2];
+  char v[VBUF][SUBN * NSUB * D * 2];
 };
 
-// NW wavefronts (4 or 8) of 32 query rows each
-template <int D, bool CAUSAL, int NW = 4, bool PACK = false>
-__device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict__ k,
+// NW wavefronts (4 or 8) of 32 query rows each; key tiles of NSUB 32-key
+// subtiles (2: 64 keys, two workgroups per CU; 1: 32 keys, whose smaller
+// register set and LDS footprint let three workgroups share a CU).  With
+// NSUB = 1 the second subtile's statements below are compiled out.
+template <int D, bool CAUSAL, int NW = 4, bool PACK = false, int NSUB = 2>
+__device__ __forceinline__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict__ k,
                              const bf16* __restrict__ v, bf16* __restrict__ o,
                              float* __restrict__ lse, int nq, int nk, float scale, int hq, int hkv,
                              int num_m_blocks, int total_blocks) {
+  constexpr int BN = SUBN * NSUB;      // keys per tile
   constexpr int BM = 32 * NW;          // query rows per workgroup
   constexpr int NT = 64 * NW;          // threads
   constexpr int DC = D / 16;           // d-chunks of 16 for QK^T
@@ -74,7 +81,7 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   constexpr int TCH = BN * CPR / NT;   // chunks per thread per tile (K and V each)
   constexpr int LSTEP = NT * 16;       // bytes of one load across the workgroup
   constexpr int TILE = BN * D * 2;     // bytes per tile
-  __shared__ FwdSmem<D> sm;
+  __shared__ FwdSmem<D, NSUB> sm;
 
   const int tid = threadIdx.x;
   // wave-uniform (an SGPR): every branch on it is a scalar branch
@@ -190,12 +197,12 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   const float sl2 = scale * kLog2e;
 
   // P of the previous tile: the B operand of its delayed PV product
-  uint32_t pprev[2][8];
-  uint32_t pnew[2][8];
+  uint32_t pprev[NSUB][8];
+  uint32_t pnew[NSUB][8];
 
   // PV product j = (kt, hh, t): A = V^T rows t of keys 32kt + 16hh .. +16,
   // two transpose reads; B = P of those keys
-  constexpr int NJ = 4 * DT;
+  constexpr int NJ = 2 * NSUB * DT;
   constexpr int VPF = 2;  // V fragments are read this many products ahead
   auto pv_read = [&](const char* vt, int j) {
     const int t = j % DT, hh = (j / DT) & 1, kt = j / (2 * DT);
@@ -210,32 +217,33 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
     acc_o[t] = mfma32(as_bf16x8(a), bop, acc_o[t]);
   };
 
-  // S^T = K Q^T for both 32-key subtiles of a tile (two interleaved chains,
-  // K fragments read KPF steps ahead)
+  // S^T = K Q^T for the NSUB 32-key subtiles of a tile (interleaved
+  // chains, K fragments read KPF steps ahead)
   auto qk = [&](const char* kt0, f32x16& s0, f32x16& s1) {
     constexpr int KPF = 2;
     s0 = f32x16{};
-    s1 = f32x16{};
+    if constexpr (NSUB == 2) s1 = f32x16{};
     u32x4 ra[DC], rb[DC];
 #pragma unroll
     for (int c = 0; c < KPF; ++c) {
       ra[c] = *reinterpret_cast<const u32x4*>(kt0 + k_off[c]);
-      rb[c] = *reinterpret_cast<const u32x4*>(kt0 + 32 * D * 2 + k_off[c]);
+      if constexpr (NSUB == 2) rb[c] = *reinterpret_cast<const u32x4*>(kt0 + 32 * D * 2 + k_off[c]);
     }
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
       if (c + KPF < DC) {
         ra[c + KPF] = *reinterpret_cast<const u32x4*>(kt0 + k_off[c + KPF]);
-        rb[c + KPF] = *reinterpret_cast<const u32x4*>(kt0 + 32 * D * 2 + k_off[c + KPF]);
+        if constexpr (NSUB == 2)
+          rb[c + KPF] = *reinterpret_cast<const u32x4*>(kt0 + 32 * D * 2 + k_off[c + KPF]);
       }
       s0 = mfma32(as_bf16x8(ra[c]), qreg[c], s0);
-      s1 = mfma32(as_bf16x8(rb[c]), qreg[c], s1);
+      if constexpr (NSUB == 2) s1 = mfma32(as_bf16x8(rb[c]), qreg[c], s1);
     }
-    sched_group(kDsRead, 2 * KPF);
+    sched_group(kDsRead, NSUB * KPF);
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
-      if (c + KPF < DC) sched_group(kDsRead, 2);
-      sched_group(kMfma, 2);
+      if (c + KPF < DC) sched_group(kDsRead, NSUB);
+      sched_group(kMfma, NSUB);
     }
   };
 
@@ -247,8 +255,10 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
       for (int r = 0; r < 16; ++r) {
         int key = kbase + 8 * (r >> 2) + 4 * g + (r & 3);
         if (key >= nk || (CAUSAL && key > qrow)) s0[r] = -INFINITY;
-        key += 32;
-        if (key >= nk || (CAUSAL && key > qrow)) s1[r] = -INFINITY;
+        if constexpr (NSUB == 2) {
+          key += 32;
+          if (key >= nk || (CAUSAL && key > qrow)) s1[r] = -INFINITY;
+        }
       }
     }
   };
@@ -262,15 +272,17 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
   auto max_piece = [&](int u, const f32x16& s0, const f32x16& s1) {
     if (u == 0) {
       mxa = max3(s0[0], s0[1], s0[2]);
-      mxb = max3(s1[0], s1[1], s1[2]);
+      if constexpr (NSUB == 2) mxb = max3(s1[0], s1[1], s1[2]);
     }
 #pragma unroll
     for (int r = (u == 0 ? 3 : 4 * u + 1); r < 4 * u + 5 && r < 15; r += 2) {
       mxa = max3(mxa, s0[r], s0[r + 1]);
-      mxb = max3(mxb, s1[r], s1[r + 1]);
+      if constexpr (NSUB == 2) mxb = max3(mxb, s1[r], s1[r + 1]);
     }
     if (u == 3) {
-      float mx = max3(mxa, mxb, max3(s0[15], s1[15], s1[15]));
+      float mx;
+      if constexpr (NSUB == 2) mx = max3(mxa, mxb, max3(s0[15], s1[15], s1[15]));
+      else mx = fmaxf(mxa, s0[15]);
       mx = max3(mx, other_half(mx), mx);
       const float m_tile = mx * sl2;  // scale > 0, so max(scale*s) = scale*max(s)
       const float m_new = fmaxf(m_run, m_tile);
@@ -283,17 +295,26 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
       grow = true;
     }
   };
-  // softmax of element pair q (0..15): half q%2 (s0 / s1), rows 2(q/2), +1;
-  // the row sums (la: s0's keys, lb: s1's) add the bf16 P that the PV
-  // product consumes
+  // softmax of element pair q, the bf16 P that the PV product consumes
+  // added into one of two row-sum chains.  NSUB = 2: pairs 0..15, half q%2
+  // (s0 / s1), rows 2(q/2), +1 (la: s0's keys, lb: s1's); NSUB = 1: pairs
+  // 0..7, elements 2q, 2q+1 of s0 (la: even pairs, lb: odd)
   auto sm_pair = [&](const f32x16& s0, const f32x16& s1, int q, float& la, float& lb) {
-    const int hf = q & 1, r = (q >> 1) * 2;
-    const float x0 = hf ? s1[r] : s0[r], x1 = hf ? s1[r + 1] : s0[r + 1];
-    const uint32_t w = pack_bf16x2(fast_exp2(__builtin_fmaf(x0, sl2, -m_use)),
-                                   fast_exp2(__builtin_fmaf(x1, sl2, -m_use)));
-    pnew[hf][r >> 1] = w;
-    if (hf) lb = add_bf16x2(w, lb);
-    else la = add_bf16x2(w, la);
+    if constexpr (NSUB == 2) {
+      const int hf = q & 1, r = (q >> 1) * 2;
+      const float x0 = hf ? s1[r] : s0[r], x1 = hf ? s1[r + 1] : s0[r + 1];
+      const uint32_t w = pack_bf16x2(fast_exp2(__builtin_fmaf(x0, sl2, -m_use)),
+                                     fast_exp2(__builtin_fmaf(x1, sl2, -m_use)));
+      pnew[hf][r >> 1] = w;
+      if (hf) lb = add_bf16x2(w, lb);
+      else la = add_bf16x2(w, la);
+    } else {
+      const uint32_t w = pack_bf16x2(fast_exp2(__builtin_fmaf(s0[2 * q], sl2, -m_use)),
+                                     fast_exp2(__builtin_fmaf(s0[2 * q + 1], sl2, -m_use)));
+      pnew[0][q] = w;
+      if (q & 1) lb = add_bf16x2(w, lb);
+      else la = add_bf16x2(w, la);
+    }
   };
   // the tile's partial row sums are checked before they join l: a tile with
   // a sum at or above 2^31 (or not finite) is redone with its maximum
@@ -304,13 +325,14 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
       la = 0.0f;
       lb = 0.0f;
 #pragma unroll
-      for (int q = 0; q < 16; ++q) sm_pair(s0, s1, q, la, lb);
+      for (int q = 0; q < 8 * NSUB; ++q) sm_pair(s0, s1, q, la, lb);
     }
     l_run += la;
     l_run2 += lb;
   };
-  // the product after which softmax pair q is issued (NJ = 16 or 8 products)
-  auto pair_slot = [](int q) { return q * NJ / 16; };
+  // the product after which softmax pair q is issued (8 NSUB pairs over NJ
+  // products)
+  auto pair_slot = [](int q) { return q * NJ / (8 * NSUB); };
   auto rescale_o = [&]() {
 #pragma unroll
     for (int t = 0; t < DT; ++t) acc_o[t] *= alpha;
@@ -338,11 +360,11 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
     for (int u = 0; u < 4; ++u) max_piece(u, s0, s1);
     grow = false;  // O is still zero: no scaling due
 #pragma unroll
-    for (int q = 0; q < 16; ++q) sm_pair(s0, s1, q, l_run, l_run2);
+    for (int q = 0; q < 8 * NSUB; ++q) sm_pair(s0, s1, q, l_run, l_run2);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       pprev[0][i] = pnew[0][i];
-      pprev[1][i] = pnew[1][i];
+      if constexpr (NSUB == 2) pprev[1][i] = pnew[1][i];
     }
     __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile 1 have landed
     __syncthreads();
@@ -383,7 +405,7 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
       if (j + VPF < NJ) va[j + VPF] = pv_read(vt, j + VPF);
       pv_mfma(j, va[j]);
 #pragma unroll
-      for (int q = 0; q < 16; ++q)
+      for (int q = 0; q < 8 * NSUB; ++q)
         if (pair_slot(q) == j) sm_pair(s0, s1, q, la, lb);
       if (j == NJ / 2 && it + 1 < n_iter)
         load_tile(it + 1, ((kb + 1) % KBUF) * TILE, ((vp + 2) % VBUF) * TILE);
@@ -393,9 +415,9 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       pin(pnew[0][i]);
-      pin(pnew[1][i]);
+      if constexpr (NSUB == 2) pin(pnew[1][i]);
       pprev[0][i] = pnew[0][i];
-      pprev[1][i] = pnew[1][i];
+      if constexpr (NSUB == 2) pprev[1][i] = pnew[1][i];
     }
     pin(l_run);
     pin(l_run2);
@@ -460,55 +482,35 @@ __device__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict_
 
 }  // namespace
 
-#define TEENY_FA2_FWD_BF16_INST(D)                                                               \
-  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
-  void teeny_fa2_fwd_bf16_d##D##_c(                                                              \
-      const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,            \
-      float scale, int hq, int hkv, int nmb, int total) {                                        \
-    fa2_fwd_bf16<D, true>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);                    \
-  }                                                                                              \
-  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
-  void teeny_fa2_fwd_bf16_d##D##_n(                                                              \
-      const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,            \
-      float scale, int hq, int hkv, int nmb, int total) {                                        \
-    fa2_fwd_bf16<D, false>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);                   \
+// One instance: name suffix, head dim, causal, wavefronts, GQA-packed, 32-key
+// subtiles per tile, wavefronts per SIMD the register budget is sized for.
+// At D = 128 the causal forms take 32-key tiles at three wavefronts per SIMD
+// (168 VGPRs, 40 KiB LDS, three workgroups per CU): 2-7 % faster than 64-key
+// tiles at two, which cover each other's MFMA and VALU phases less well;
+// the bidirectional form keeps 64-key tiles (at 168 VGPRs it spills and ran
+// 3 % slower).  At D = 64 the 64-key tiles already fit three wavefronts per
+// SIMD (149-165 VGPRs): 5-6 % faster than at two, with the same output bits.
+#define TEENY_FA2_FWD_BF16_K(SFX, D, C, NW, PACK, NSUB, WPE)                                   \
+  extern "C" __global__ __launch_bounds__(64 * NW)                                               \
+      __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void teeny_fa2_fwd_bf16_d##D##_##SFX(       \
+          const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,        \
+          float scale, int hq, int hkv, int nmb, int total) {                                    \
+    fa2_fwd_bf16<D, C, NW, PACK, NSUB>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);       \
   }
 
-TEENY_FA2_FWD_BF16_INST(64)
-TEENY_FA2_FWD_BF16_INST(128)
+// 4 wavefronts, 128 query rows of one (b, q head) per workgroup
+TEENY_FA2_FWD_BF16_K(c, 64, true, 4, false, 2, 3)
+TEENY_FA2_FWD_BF16_K(n, 64, false, 4, false, 2, 3)
+TEENY_FA2_FWD_BF16_K(c, 128, true, 4, false, 1, 3)
+TEENY_FA2_FWD_BF16_K(n, 128, false, 4, false, 2, 2)
 
 // 8 wavefronts, 256 query rows per workgroup (long GQA sequences)
-#define TEENY_FA2_FWD_BF16_W8_INST(D, C, CZ)                                                    \
-  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
-  void teeny_fa2_fwd_bf16_d##D##_##CZ##_w8(                                                      \
-      const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,            \
-      float scale, int hq, int hkv, int nmb, int total) {                                        \
-    fa2_fwd_bf16<D, C, 8>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);                    \
-  }
-TEENY_FA2_FWD_BF16_W8_INST(128, true, c)
-TEENY_FA2_FWD_BF16_W8_INST(128, false, n)
+TEENY_FA2_FWD_BF16_K(c_w8, 128, true, 8, false, 2, 2)
+TEENY_FA2_FWD_BF16_K(n_w8, 128, false, 8, false, 2, 2)
 
 // GQA-packed: one workgroup per (b, kv head, 32 query rows), wavefront w on
-// q head kv head * 4 + w (hq = 4 hkv); every wavefront of a causal block
+// q head kv head * NW + w (hq = NW hkv); every wavefront of a causal block
 // ends on the same row, so none waits out the block's last tiles
-#define TEENY_FA2_FWD_BF16_G4_INST(D, C, CZ)                                                    \
-  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
-  void teeny_fa2_fwd_bf16_d##D##_##CZ##_g4(                                                      \
-      const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,            \
-      float scale, int hq, int hkv, int nmb, int total) {                                        \
-    fa2_fwd_bf16<D, C, 4, true>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);              \
-  }
-
-TEENY_FA2_FWD_BF16_G4_INST(64, true, c)
-TEENY_FA2_FWD_BF16_G4_INST(128, true, c)
-
-// 8 wavefronts: q heads kv head * 8 + w (hq = 8 hkv)
-#define TEENY_FA2_FWD_BF16_G8_INST(D, C, CZ)                                                    \
-  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
-  void teeny_fa2_fwd_bf16_d##D##_##CZ##_g8(                                                      \
-      const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,            \
-      float scale, int hq, int hkv, int nmb, int total) {                                        \
-    fa2_fwd_bf16<D, C, 8, true>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);              \
-  }
-
-TEENY_FA2_FWD_BF16_G8_INST(128, true, c)
+TEENY_FA2_FWD_BF16_K(c_g4, 64, true, 4, true, 2, 3)
+TEENY_FA2_FWD_BF16_K(c_g4, 128, true, 4, true, 1, 3)
+TEENY_FA2_FWD_BF16_K(c_g8, 128, true, 8, true, 2, 2)
