@@ -143,13 +143,14 @@ int teeny_flash_attn2_bwd(const void* q, const void* k, const void* v, const voi
  * (its executor sizes caches from RuntimeOp::param_shapes, flash_attn2.rs:449-457). */
 size_t teeny_flash_attn2_bwd_workspace_bytes(int n_ctx_q, int batch, int n_heads_q, int head_dim,
                                              int dtype);
-/* The workspace that also lets a bf16 GQA backward with few key blocks
- * (fewer 128-key blocks x batch x kv heads than two per CU) and 1024 or
- * more query rows split each
- * group's q heads over 2 or 4 dK/dV workgroups, whose fp32 partial sums a
- * merge kernel adds in a fixed order; otherwise equal to the above.  With a
- * smaller workspace the backward runs unsplit.  No counterpart in the
- * reference. */
+/* The workspace that also lets a causal bf16 GQA backward of 12288 or more
+ * query rows with few key blocks (at most four 128-key blocks x batch x kv
+ * heads per CU) and an even group (Hq / Hkv) split each group's q heads over
+ * 4 dK/dV workgroups (2 if 4 does not divide the group), whose fp32 partial
+ * sums a merge kernel adds in a fixed order; otherwise equal to the above.
+ * With a smaller workspace such a backward runs its dK/dV in two wavefront
+ * groups per workgroup instead (the form used from 2048 to 12287 query rows
+ * of even groups).  No counterpart in the reference. */
 size_t teeny_flash_attn2_bwd_workspace_bytes_gqa(int n_ctx_q, int n_ctx_k, int batch,
                                                  int n_heads_q, int n_heads_kv, int head_dim,
                                                  int dtype);

@@ -334,24 +334,36 @@ int device_cus() {
   return n;
 }
 
-// bf16 dK/dV: into how many workgroups each GQA group's q heads are split.
-// The kernel runs two workgroups per CU and its causal key blocks range
-// from one to n_ctx_q / 128 units of work; with no more workgroups than
-// slots, the heaviest block alone sets the time, so the heads are split
-// (up to 4 ways) while the workgroups still fit twice over.  Below 1024
-// query rows the walks are short and the fp32 partials and their merge cost
-// more than the split saves (measured 15-21 % slower at 512 rows, 7-33 %
-// faster at 2048-8191).
-int dkdv_hsplit(int n_ctx_q, int n_ctx_k, int batch, int hq, int hkv, int dtype) {
-  if (dtype != TEENY_BF16 || n_ctx_q < 1024) return 1;
-  const long slots = 2L * device_cus();
-  long wgs = (long)((n_ctx_k + 127) / 128) * batch * hkv;
-  int split = 1;
-  while (split < 4 && (hq / hkv) % (2 * split) == 0 && wgs <= slots) {
-    split *= 2;
-    wgs *= 2;
-  }
-  return split;
+// bf16 dK/dV: how each GQA group's q heads are shared out.  A workgroup
+// owns 128 keys of a (b, kv head) and walks the query blocks of its q heads
+// (causal: key block nb sees n_ctx_q / 128 - nb of them), so with few key
+// blocks the heaviest walks set the time.  Two ways to shorten them:
+//   groups = 2: the workgroup is two groups of 4 wavefronts on the same
+//     keys, each walking half of the q heads, their sums added through LDS
+//     (one workgroup per CU);
+//   split > 1: the q heads are split over `split` workgroups whose fp32
+//     partial sums a merge kernel adds in a fixed order (needs the larger
+//     workspace).
+// Measured (MI355X, causal, Hq/Hkv 4 and 8, D 64 and 128, same-box A/B of
+// every combination): two groups are 1.02-1.45x the plain kernel from 2048
+// to 8191 query rows and at least as fast as any split there; from 12288
+// rows of one sequence the 4-way split is 1.05-1.13x and the two groups
+// 0.98-1.05x; at 512 and 1024 rows, for the bidirectional kernel and with
+// many key-block workgroups (B2 S8192) the plain kernel is fastest.
+struct DkdvPlan {
+  int groups, split;
+};
+DkdvPlan dkdv_plan(bool causal, int n_ctx_q, int n_ctx_k, int batch, int hq, int hkv,
+                   int dtype) {
+  DkdvPlan p{1, 1};
+  const int group = hq / hkv;
+  if (dtype != TEENY_BF16 || !causal || group % 2 != 0 || n_ctx_q < 2048) return p;
+  const long wgs = (long)((n_ctx_k + 127) / 128) * batch * hkv;
+  if (n_ctx_q >= 12288 && wgs <= 4L * device_cus())
+    p.split = group % 4 == 0 ? 4 : 2;
+  else
+    p.groups = 2;
+  return p;
 }
 
 size_t dkdv_split_bytes(int n_ctx_k, int batch, int hkv, int head_dim, int split) {
@@ -396,21 +408,24 @@ int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void
     rc = launch(name, dim3(tot), dim3(256), 0, stream, a2);
     if (rc) return rc;
     // dK, dV: one workgroup per 128 keys of a (b, kv head) and share of the
-    // group's q heads (the split needs the larger workspace; without it the
-    // heads are not split)
-    int hsplit = dkdv_hsplit(n_ctx_q, n_ctx_k, batch, hq, hkv, dtype);
+    // group's q heads (a split needs the larger workspace; without it the
+    // two-group kernel runs instead, the group being even)
+    DkdvPlan plan = dkdv_plan(causal, n_ctx_q, n_ctx_k, batch, hq, hkv, dtype);
     const size_t base = fa2_bwd_ws(n_ctx_q, batch, hq, head_dim, dtype);
-    if (workspace_bytes < base + dkdv_split_bytes(n_ctx_k, batch, hkv, head_dim, hsplit))
-      hsplit = 1;
+    if (plan.split > 1 &&
+        workspace_bytes < base + dkdv_split_bytes(n_ctx_k, batch, hkv, head_dim, plan.split))
+      plan = DkdvPlan{2, 1};
+    int hsplit = plan.split;
     float* part = hsplit > 1 ? (float*)((char*)workspace + base) : nullptr;
     int nnb = (n_ctx_k + 127) / 128;
     total = (long)nnb * batch * hkv * hsplit;
     if (total >= (1L << 31)) return TEENY_ERR_INVALID_SHAPE;
     tot = (int)total;
-    snprintf(name, sizeof name, "teeny_fa2_bwd_dkdv_bf16_d%d_%s%s", head_dim, cz, gsfx);
+    snprintf(name, sizeof name, "teeny_fa2_bwd_dkdv_bf16_d%d_%s%s%s", head_dim, cz,
+             plan.groups == 2 ? "_hg2" : "", gsfx);
     void* a1[] = {&q,       &k,       &v,     &dout, &ld,  &dk,  &dv,  &n_ctx_q,
                   &n_ctx_k, &scale,   &hq,    &hkv,  &nnb, &tot, &hsplit, &part};
-    rc = launch(name, dim3(tot), dim3(256), 0, stream, a1);
+    rc = launch(name, dim3(tot), dim3(256 * plan.groups), 0, stream, a1);
     if (rc || hsplit == 1) return rc;
     long n = (long)batch * hkv * n_ctx_k * head_dim;  // a multiple of 8
     void* a3[] = {&part, &dk, &dv, &n, &hsplit, &scale};
@@ -588,7 +603,9 @@ size_t teeny_flash_attn2_bwd_workspace_bytes_gqa(int n_ctx_q, int n_ctx_k, int b
       head_dim <= 0 || n_heads_q % n_heads_kv != 0)
     return 0;
   dtype &= ~TEENY_GRAD_F32;
-  const int split = dkdv_hsplit(n_ctx_q, n_ctx_k, batch, n_heads_q, n_heads_kv, dtype);
+  // the split is planned only for the causal backward
+  const int split =
+      dkdv_plan(true, n_ctx_q, n_ctx_k, batch, n_heads_q, n_heads_kv, dtype).split;
   return fa2_bwd_ws(n_ctx_q, batch, n_heads_q, head_dim, dtype) +
          dkdv_split_bytes(n_ctx_k, batch, n_heads_kv, head_dim, split);
 }

@@ -69,25 +69,29 @@ struct __attribute__((aligned(16))) DkdvSmem {
 // (more workgroups when few key blocks would leave CUs idle behind the
 // heaviest causal block); each writes its fp32 dK^T, dV^T sums to
 // part[2][hsplit][B * Hkv][nk][D] (dK unscaled), merged by fa2_dkdv_merge.
-template <int D, bool CAUSAL, typename GT>
-__device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict__ k,
-                             const bf16* __restrict__ v, const bf16* __restrict__ dout,
-                             const float* __restrict__ ld, GT* __restrict__ dk,
-                             GT* __restrict__ dv, int nq, int nk, float scale, int hq, int hkv,
-                             int num_n_blocks, int total_blocks, int hsplit,
-                             float* __restrict__ part) {
+// NG = 2: the workgroup is two groups of 4 wavefronts (GRP 0 and 1, the
+// kernel branches once on it) on the same 128 keys, each walking half of
+// the workgroup's q heads in its own copy of the LDS block (smg[GRP]; a
+// compile-time copy, so every LDS address keeps its immediate offset); at
+// the end group 1's sums are added to group 0's through LDS, which stores.
+template <int D, bool CAUSAL, typename GT, int NG = 1, int GRP = 0>
+__device__ __forceinline__ void fa2_bwd_dkdv(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const bf16* __restrict__ dout, const float* __restrict__ ld, GT* __restrict__ dk,
+    GT* __restrict__ dv, int nq, int nk, float scale, int hq, int hkv, int num_n_blocks,
+    int total_blocks, int hsplit, float* __restrict__ part, DkdvSmem<D>* smg) {
   constexpr int DC = D / 16;            // d-chunks of 16 (QK^T, dO V^T)
   constexpr int DT = D / 32;            // d-tiles of 32 (dK^T, dV^T)
   constexpr int CPR = D / 8;            // 16-byte chunks per row
   constexpr int TCH = BM * CPR / 256;   // chunks per thread of a Q or dO tile
   constexpr int VCH = BN * CPR / 256;   // chunks per thread of the V block
-  __shared__ DkdvSmem<D> sm;
+  DkdvSmem<D>& sm = smg[GRP];
 
   // fp32 gradients: P and dS also enter the products as a second, low bf16
   // part (x = hi + lo, hi = bf16(x), lo = bf16(x - hi)), so their bf16
   // operand rounding (2^-9 relative) drops to 2^-17
   constexpr bool PRECISE = std::is_same<GT, float>::value;
-  const int tid = threadIdx.x;
+  const int tid = NG == 1 ? (int)threadIdx.x : (int)threadIdx.x & 255;  // within the group
   // wave-uniform (an SGPR): every branch on it is a scalar branch
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
@@ -97,8 +101,8 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
   pair_order(id, num_n_blocks, total_blocks / num_n_blocks, hh, nb);
   const int kvh = hh / hsplit, hs = hh - kvh * hsplit;
   const int b = kvh / hkv, hk = kvh - b * hkv;
-  const int group = hq / hkv / hsplit;  // q heads walked by this workgroup
-  const int head0 = hk * (hq / hkv) + hs * group;
+  const int group = hq / hkv / hsplit / NG;  // q heads walked by this wavefront group
+  const int head0 = hk * (hq / hkv) + (hs * NG + GRP) * group;
   const int n0 = nb * BN;
   const int kw0 = n0 + 32 * wave;  // this wave's first key
   const int mykey = kw0 + l32;
@@ -335,6 +339,35 @@ __device__ void fa2_bwd_dkdv(const bf16* __restrict__ q, const bf16* __restrict_
     __syncthreads();
   }
 
+  if constexpr (NG == 2) {
+    // group 1's sums into group 0's through LDS, dK^T then dV^T (16 bytes
+    // per lane and step, consecutive lanes consecutive); the walk's last
+    // barrier has retired every tile read
+    f32x4* x = reinterpret_cast<f32x4*>(smg) + wave * DT * 4 * 64 + lane;
+    auto exchange = [&](f32x16(&acc)[DT]) {
+      if constexpr (GRP == 1)
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            x[(t * 4 + j) * 64] =
+                f32x4{acc[t][4 * j], acc[t][4 * j + 1], acc[t][4 * j + 2], acc[t][4 * j + 3]};
+      __syncthreads();
+      if constexpr (GRP == 0)
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const f32x4 y = x[(t * 4 + j) * 64];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t][4 * j + i] += y[i];
+          }
+      __syncthreads();
+    };
+    exchange(dk_acc);
+    exchange(dv_acc);
+    if constexpr (GRP == 1) return;
+  }
   // ---- dK = scale * dK^T, dV = dV^T, lane = key, 16 d values per tile -------
   if (hsplit > 1) {  // fp32 sums of this workgroup's heads
     if (mykey < nk) {
@@ -764,8 +797,9 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
       const bf16* q, const bf16* k, const bf16* v, const bf16* dout, const float* ld, GT* dk,   \
       GT* dv, int nq, int nk, float scale, int hq, int hkv, int nnb, int total, int hsplit,     \
       float* part) {                                                                            \
+    __shared__ DkdvSmem<D> sm[1];                                                               \
     fa2_bwd_dkdv<D, CAUSAL, GT>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb, total, \
-                                hsplit, part);                                                  \
+                                hsplit, part, sm);                                              \
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
   void teeny_fa2_bwd_dq_bf16_d##D##_##CZ##SFX(                                                  \
@@ -784,6 +818,28 @@ TEENY_FA2_BWD_BF16_INST(64, c, true, float, _g32)
 TEENY_FA2_BWD_BF16_INST(64, n, false, float, _g32)
 TEENY_FA2_BWD_BF16_INST(128, c, true, float, _g32)
 TEENY_FA2_BWD_BF16_INST(128, n, false, float, _g32)
+
+// dK/dV of causal GQA with an even group, in two wavefront groups (512
+// threads, one workgroup per CU)
+#define TEENY_FA2_BWD_DKDV_HG2_INST(D, GT, SFX)                                                  \
+  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
+  void teeny_fa2_bwd_dkdv_bf16_d##D##_c_hg2##SFX(                                               \
+      const bf16* q, const bf16* k, const bf16* v, const bf16* dout, const float* ld, GT* dk,   \
+      GT* dv, int nq, int nk, float scale, int hq, int hkv, int nnb, int total, int hsplit,     \
+      float* part) {                                                                            \
+    __shared__ DkdvSmem<D> sm[2];                                                               \
+    if (threadIdx.x >= 256)                                                                     \
+      fa2_bwd_dkdv<D, true, GT, 2, 1>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb,  \
+                                      total, hsplit, part, sm);                                 \
+    else                                                                                        \
+      fa2_bwd_dkdv<D, true, GT, 2, 0>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb,  \
+                                      total, hsplit, part, sm);                                 \
+  }
+
+TEENY_FA2_BWD_DKDV_HG2_INST(64, bf16, )
+TEENY_FA2_BWD_DKDV_HG2_INST(128, bf16, )
+TEENY_FA2_BWD_DKDV_HG2_INST(64, float, _g32)
+TEENY_FA2_BWD_DKDV_HG2_INST(128, float, _g32)
 
 // dQ of causal GQA groups of 4, packed (hq = 4 hkv)
 #define TEENY_FA2_BWD_DQ_G4_INST(D, GT, SFX)                                                     \

@@ -74,7 +74,8 @@ def test_fa2_grad_f32_flag(L):
         assert L.teeny_flash_attn2_bwd_workspace_bytes(*args, BF16 | GRAD_F32) == \
             L.teeny_flash_attn2_bwd_workspace_bytes(*args, BF16)
     f = L.teeny_flash_attn2_bwd_workspace_bytes_gqa
-    assert f(8191, 8191, 1, 64, 8, 128, BF16 | GRAD_F32) == f(8191, 8191, 1, 64, 8, 128, BF16)
+    assert f(16384, 16384, 1, 64, 8, 128, BF16 | GRAD_F32) == \
+        f(16384, 16384, 1, 64, 8, 128, BF16)
     # validation still applies to the flagged dtype
     rc = L.teeny_causal_flash_attn2_bwd(P, P, P, P, P, P, P, P, P, 128, 128, 0.125, 1, 4, 4, 32,
                                         BF16 | GRAD_F32, P, 1 << 20, None)
@@ -96,24 +97,28 @@ def test_noalloc_bwd_refuses_beyond_scratch(L):
 
 def test_fa2_bwd_workspace_gqa(L):
     """The larger workspace that allows the dK/dV head split: only for bf16
-    GQA with 1024+ query rows and few key blocks (here 64 blocks x 8 kv heads = 512 workgroups,
-    two per CU of a 256-CU device without a GPU to ask), fp32 dK and dV
-    partials for 2 splits on top of the base workspace."""
+    GQA with an even group, 12288+ query rows and few key blocks (at most
+    four 128-key blocks x batch x kv heads per CU of a 256-CU device without
+    a GPU to ask): fp32 dK and dV partials for 4 splits (2 when 4 does not
+    divide the group) on top of the base workspace."""
     f = L.teeny_flash_attn2_bwd_workspace_bytes_gqa
-    base = L.teeny_flash_attn2_bwd_workspace_bytes(8191, 1, 64, 128, BF16)
-    assert f(8191, 8191, 1, 64, 8, 128, BF16) >= base + 2 * 2 * 8 * 8191 * 128 * 4
-    # MHA, many key blocks, fp32: nothing to split
-    assert f(4096, 4096, 8, 32, 32, 128, BF16) == L.teeny_flash_attn2_bwd_workspace_bytes(
-        4096, 8, 32, 128, BF16)
-    assert f(16384, 16384, 1, 64, 8, 128, BF16) == L.teeny_flash_attn2_bwd_workspace_bytes(
-        16384, 1, 64, 128, BF16)
-    # fewer than 1024 query rows: short walks, no split (B16 Hq32 Hkv8 S512)
-    assert f(512, 512, 16, 32, 8, 128, BF16) == L.teeny_flash_attn2_bwd_workspace_bytes(
-        512, 16, 32, 128, BF16)
-    assert f(1024, 1024, 4, 32, 8, 128, BF16) > L.teeny_flash_attn2_bwd_workspace_bytes(
-        1024, 4, 32, 128, BF16)
-    assert f(128, 128, 1, 4, 2, 64, F32) == L.teeny_flash_attn2_bwd_workspace_bytes(
-        128, 1, 4, 64, F32)
+    base = L.teeny_flash_attn2_bwd_workspace_bytes
+    # B1 Hq64 Hkv8 S16384: 128 blocks x 8 kv heads = 1024 workgroups, split 4
+    assert f(16384, 16384, 1, 64, 8, 128, BF16) == base(16384, 1, 64, 128, BF16) + \
+        2 * 4 * 8 * 16384 * 128 * 4
+    # group of 2: split 2 (the shape the no-allocation test runs)
+    assert f(12288, 12288, 1, 2, 1, 64, BF16) == base(12288, 1, 2, 64, BF16) + \
+        2 * 2 * 1 * 12288 * 64 * 4
+    # 2048-12287 rows (two wavefront groups, no partials), short walks, MHA,
+    # odd groups, many key blocks, fp32: nothing to split
+    for args in ((8191, 8191, 1, 64, 8, 128), (4096, 4096, 2, 32, 8, 128),
+                 (1024, 1024, 4, 32, 8, 128), (512, 512, 16, 32, 8, 128),
+                 (16384, 16384, 1, 32, 32, 128), (16384, 16384, 1, 24, 8, 128),
+                 (16384, 16384, 2, 64, 8, 128)):
+        Sq, Sk, B, Hq, Hkv, D = args
+        assert f(*args, BF16) == base(Sq, B, Hq, D, BF16), args
+    assert f(128, 128, 1, 4, 2, 64, F32) == base(128, 1, 4, 64, F32)
+    assert f(16384, 16384, 1, 64, 8, 128, F32) == base(16384, 1, 64, 128, F32)
     assert f(128, 128, 1, 6, 4, 64, BF16) == 0  # Hq % Hkv != 0
     assert f(0, 128, 1, 4, 2, 64, BF16) == 0
 

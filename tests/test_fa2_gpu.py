@@ -230,37 +230,62 @@ def test_fa2_bf16_bwd(cuda, shape, causal):
         assert rel_l2(host(a), w) <= rel_l2(host(b), w)
 
 
-@pytest.mark.parametrize("shape", [(2, 8, 2, 1100, 1100, 128), (1, 8, 1, 1025, 1025, 128),
-                                   (1, 16, 2, 1200, 1150, 64)])
-@pytest.mark.parametrize("causal", [True, False])
-def test_fa2_bf16_bwd_gqa_split(cuda, shape, causal):
-    """dK/dV with each GQA group's q heads split over 2-4 workgroups (the
-    workspace of teeny_flash_attn2_bwd_workspace_bytes_gqa; fp32 partials
-    merged in a fixed order) and unsplit (the smaller workspace): both match
-    the oracle, dQ is the same kernel either way, and the two dK/dV differ by
-    at most the bf16 rounding of the summation order."""
+@pytest.mark.parametrize("shape", [(1, 4, 2, 2048, 2048, 64), (1, 2, 1, 2100, 2050, 128),
+                                   (2, 4, 2, 2200, 2200, 64)])
+def test_fa2_bf16_bwd_gqa_two_groups(cuda, shape):
+    """Causal GQA with an even group and 2048+ query rows: dK/dV in two
+    wavefront groups per workgroup, each walking half of the q heads of the
+    same keys, their sums added through LDS; no partial sums, so the larger
+    workspace equals the base one.  bf16 and fp32 gradients against the
+    oracle."""
     B, Hq, Hkv, Sq, Sk, D = shape
     q, k, v, do = inputs(50, *shape, bf16=True)
     scale = 1.0 / math.sqrt(D)
     qd, kd, vd, dod = (dev(t, torch.bfloat16) for t in (q, k, v, do))
-    o, lse = ops.flash_attn2_fwd(qd, kd, vd, scale, causal)
-    small = ops.flash_attn2_bwd_workspace_bytes(qd)
-    big = ops.flash_attn2_bwd_workspace_bytes(qd, kd)
-    # these shapes have few key blocks and 1024+ query rows: the split applies
-    assert big > small
+    o, lse = ops.flash_attn2_fwd(qd, kd, vd, scale, True)
+    assert ops.flash_attn2_bwd_workspace_bytes(qd, kd) == ops.flash_attn2_bwd_workspace_bytes(qd)
+    dq, dk, dv = ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod, scale, True)
+    g32 = ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod, scale, True, grad_f32=True)
+    dqe, dke, dve = O.fa2_bwd(q, k, v, host(o), do, host(lse), scale, True)
+    for name, got, w in zip(("dQ", "dK", "dV"), (dq, dk, dv), (dqe, dke, dve)):
+        check_bf16(name, host(got), w)
+    for name, got, w in zip(("dQ", "dK", "dV"), g32, (dqe, dke, dve)):
+        check_flat(name + " (fp32)", host(got), w)
+
+
+@pytest.mark.parametrize("grad_f32", [False, True])
+def test_fa2_bf16_bwd_gqa_split(cuda, grad_f32):
+    """B1 Hq2 Hkv1 S12288 D64 causal (a group of 2, 96 key blocks): with the
+    workspace of teeny_flash_attn2_bwd_workspace_bytes_gqa each group's q
+    heads split over 2 dK/dV workgroups (fp32 partials merged in a fixed
+    order); with the base workspace the two-group kernel runs instead.  dQ
+    is the same kernel either way; dK and dV agree to the bf16 rounding of
+    the summation order (or closer, for fp32 gradients).  The split against
+    the oracle: the B1 Hq64 Hkv8 S16384 whole-group test (4 splits)."""
+    B, Hq, Hkv, S, D = 1, 2, 1, 12288, 64
+    gen = torch.Generator(device="cuda").manual_seed(51)
+    q, do = (torch.randn(B, Hq, S, D, generator=gen, device="cuda").to(torch.bfloat16)
+             for _ in range(2))
+    k, v = (torch.randn(B, Hkv, S, D, generator=gen, device="cuda").to(torch.bfloat16)
+            for _ in range(2))
+    scale = 1.0 / math.sqrt(D)
+    o, lse = ops.flash_attn2_fwd(q, k, v, scale, True)
+    small = ops.flash_attn2_bwd_workspace_bytes(q)
+    big = ops.flash_attn2_bwd_workspace_bytes(q, k)
+    assert big == small + 2 * 2 * B * Hkv * S * D * 4
     outs = []
     for n in (small, big):
+        print(f"  workspace {n} bytes, grad_f32={grad_f32}", flush=True)
         ws = torch.empty(n, dtype=torch.uint8, device="cuda")
-        outs.append(ops.flash_attn2_bwd(qd, kd, vd, o, lse, dod, scale, causal, workspace=ws))
-    dqe, dke, dve = O.fa2_bwd(q, k, v, host(o), do, host(lse), scale, causal)
-    for dq, dk, dv in outs:
-        check_bf16("dQ", host(dq), dqe)
-        check_bf16("dK", host(dk), dke)
-        check_bf16("dV", host(dv), dve)
+        outs.append(ops.flash_attn2_bwd(q, k, v, o, lse, do, scale, True, workspace=ws,
+                                        grad_f32=grad_f32))
+    torch.cuda.synchronize()
     assert torch.equal(outs[0][0], outs[1][0])
+    tol = 2.0 ** -20 if grad_f32 else 2.0 ** -7
     for a, b in ((outs[0][1], outs[1][1]), (outs[0][2], outs[1][2])):
         a, b = host(a), host(b)
-        assert np.all(np.abs(a - b) <= np.abs(a) * 2.0 ** -7 + 1e-6)
+        assert np.isfinite(a).all() and np.isfinite(b).all()
+        assert np.all(np.abs(a - b) <= np.abs(a) * tol + 1e-6)
 
 
 def _random_shapes(n, seed=2026):
@@ -374,8 +399,9 @@ def test_fa2_bf16_c3_full_size(cuda):
 
 @pytest.mark.parametrize("S", [16384, 8191])
 def test_fa2_bf16_c5_long_gqa(cuda, S):
-    """B1 Hq64 Hkv8 D128 causal, 1% of K rows x8; S = 16384 and ragged 8191
-    (the latter runs the dK/dV head split and its fp32 merge): one whole
+    """B1 Hq64 Hkv8 D128 causal, 1% of K rows x8; S = 16384 (each group's q
+    heads split over 4 dK/dV workgroups, fp32 partials and their merge) and
+    ragged 8191 (dK/dV in two wavefront groups per workgroup): one whole
     GQA group of 8 q heads."""
     _group_check(1, 64, 8, S, 128, seed=8, spike=True, groups=[(0, 5)])
 
@@ -383,7 +409,7 @@ def test_fa2_bf16_c5_long_gqa(cuda, S):
 @pytest.mark.parametrize("B,S,groups", [(2, 4096, [(1, 7)]), (16, 512, [(15, 3)])])
 def test_fa2_bf16_gqa4_packed_group(cuda, B, S, groups):
     """Causal GQA groups of 4 (Hq32 Hkv8 D128), which run the GQA-packed
-    forward and dQ: B2 S4096 (its dK/dV also splits each group's q heads
-    over two workgroups) and the Llama-3-8B prefill's B16 S512 (no split
-    below 1024 rows); one whole group each, 1% of K rows x8."""
+    forward and dQ: B2 S4096 (its dK/dV runs in two wavefront groups per
+    workgroup) and the Llama-3-8B prefill's B16 S512 (one group below 2048
+    rows); one whole group each, 1% of K rows x8."""
     _group_check(B, 32, 8, S, 128, seed=9 + S, spike=True, groups=groups)
