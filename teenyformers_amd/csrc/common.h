@@ -133,17 +133,28 @@ DEVI float wave_max(float v) {
   return v;
 }
 
-// Order of the (head, block) work items behind the remapped ids: heads two
-// at a time, the blocks of a pair interleaved heaviest first.  Causal blocks
-// differ in cost by up to n_blocks x; taken head by head (heaviest first),
-// the heaviest blocks of an XCD's last head started last and finished ~5 %
-// after the rest at 32 blocks per head, while pairs keep the workgroups in
-// flight on ~2 heads' K/V as before.  Pairs only when every XCD's contiguous
-// share of ids holds whole pairs (n_heads a multiple of 16): a pair split
-// between two XCDs would hand one of them all the heavy blocks.  rank 0 is a
-// head's heaviest block.  Bijective on [0, n_heads * n_blocks).
+// Order of the (head, block) work items behind the remapped ids: heads in
+// groups of G, the blocks of a group interleaved heaviest first.  Causal
+// blocks differ in cost by up to n_blocks x; taken head by head (heaviest
+// first), the heaviest blocks of an XCD's last head started last and
+// finished ~5 % after the rest at 32 blocks per head.  Interleaving G heads
+// starts the next group's heavy blocks while the previous group's light
+// ones run, keeping workgroups in flight on a few heads' K/V.  A schedule
+// model of an XCD's slots (workgroup time = fixed + per-tile cost, both
+// measured) puts the forward at 1.06 x the ideal makespan with pairs and
+// 1.02 x with groups of 4 (B8 H32 S4096, 96 slots), 1.25 x and 1.11 x at
+// B16 Hq32 Hkv8 S512, with the same heads in flight (measured: 1.01 x and
+// 1.06 x); the backward kernels' 64 slots per XCD reach the ideal with
+// pairs.  G is the largest power of
+// two up to GMAX for which every XCD's contiguous share of ids holds whole
+// groups (n_heads a multiple of 8 G): a group split between two XCDs would
+// hand one of them all the heavy blocks.  rank 0 is a head's heaviest
+// block.  Bijective on [0, n_heads * n_blocks).
+template <int GMAX = 2>
 DEVI void pair_order(int id, int n_blocks, int n_heads, int& head, int& rank) {
-  const int gsz = n_heads % (2 * TEENY_NUM_XCD) == 0 ? 2 : 1;
+  int gsz = 1;
+  if (GMAX >= 4 && n_heads % (4 * TEENY_NUM_XCD) == 0) gsz = 4;
+  else if (GMAX >= 2 && n_heads % (2 * TEENY_NUM_XCD) == 0) gsz = 2;
   const int grp = id / (gsz * n_blocks);
   const int r = id - grp * gsz * n_blocks;
   head = gsz * grp + r % gsz;
