@@ -465,21 +465,49 @@ __device__ __forceinline__ void fa2_fwd_bf16(const bf16* __restrict__ q, const b
   // ---- epilogue ----
   l_run += l_run2;
   const float l_tot = l_run + other_half(l_run);
-  if (qrow < nq) {
-    const float inv = 1.0f / l_tot;
-    bf16* orow = o + ((long)bhq * nq + qrow) * D;
+  const float inv = 1.0f / l_tot;  // rows past nq: never stored
+  // O goes through LDS (the K/V buffers, free once every wavefront's last PV
+  // product has read its tile): each wavefront writes its 32 x D tile, the
+  // 16-byte chunk c of row r at chunk c ^ (r % CPR) of that row, and reads it
+  // back a whole row per CPR lanes, so one store writes 64 / CPR complete
+  // rows instead of 32 scattered 16-byte pieces (stored straight from the
+  // accumulators, the O rows kept each workgroup ~2 us longer on its CU)
+  static_assert(sizeof(FwdSmem<D, NSUB>) >= NW * 32 * D * 2, "O tiles fit the K/V buffers");
+  constexpr int RPI = 64 / CPR;  // rows per store
+  __builtin_amdgcn_s_waitcnt(kVmWaitLgkm0<63>());  // this wavefront's LDS reads
+  barrier_only();
+  char* ot = reinterpret_cast<char*>(&sm) + wave * (32 * D * 2);
+  // byte offsets, formed here (the empty asm keeps them out of the loop,
+  // where they would be live across it): the write of chunk c is
+  // wa ^ (c << 4) (row l32, half g), the read of store kk is
+  // (ra ^ ((kk % (CPR / RPI)) * RPI << 4)) + kk * RPI * 2 D (row kk RPI +
+  // lane / CPR, chunk lane % CPR), both XORs on bits 4.. of a row's chunk
+  // index only
+  const int ln = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int lr = ln & 31;
+  int wa = lr * (2 * D) + 8 * (ln >> 5) + ((lr & (CPR - 1)) << 4);
+  int ra = (ln / CPR) * (2 * D) + (((ln % CPR) ^ (ln / CPR)) << 4);
+  int sa = (ln / CPR) * D + 8 * (ln % CPR);  // element offset of the lane's store
+  asm volatile("" : "+v"(wa), "+v"(ra), "+v"(sa));
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
+  for (int t = 0; t < DT; ++t) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int d = 32 * t + 8 * j + 4 * g;
-        u32x2 w = {pack_bf16x2(acc_o[t][4 * j] * inv, acc_o[t][4 * j + 1] * inv),
-                   pack_bf16x2(acc_o[t][4 * j + 2] * inv, acc_o[t][4 * j + 3] * inv)};
-        *reinterpret_cast<u32x2*>(orow + d) = w;
-      }
+    for (int j = 0; j < 4; ++j) {
+      // this lane's d = 32 t + 8 j + 4 g .. + 3: half g of chunk 4 t + j
+      const u32x2 w = {pack_bf16x2(acc_o[t][4 * j] * inv, acc_o[t][4 * j + 1] * inv),
+                       pack_bf16x2(acc_o[t][4 * j + 2] * inv, acc_o[t][4 * j + 3] * inv)};
+      *reinterpret_cast<u32x2*>(ot + (wa ^ ((4 * t + j) << 4))) = w;
     }
-    if (g == 0) lse[(long)bhq * nq + qrow] = (m_run + __log2f(l_tot)) * kLn2;
   }
+  bf16* ob = o + ((long)bhq * nq + wrow0) * D;
+#pragma unroll
+  for (int kk = 0; kk < 32 / RPI; ++kk) {
+    const u32x4 val = *reinterpret_cast<const u32x4*>(
+        ot + (ra ^ (((kk % (CPR / RPI)) * RPI) << 4)) + kk * RPI * 2 * D);
+    if (wrow0 + kk * RPI + ln / CPR < nq)
+      *reinterpret_cast<u32x4*>(ob + kk * RPI * D + sa) = val;
+  }
+  if (qrow < nq && g == 0) lse[(long)bhq * nq + qrow] = (m_run + __log2f(l_tot)) * kLn2;
 }
 
 }  // namespace
