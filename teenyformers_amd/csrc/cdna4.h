@@ -115,3 +115,50 @@ __device__ __forceinline__ void unroll_tiles(F&& f) {
     unroll_tiles<B + 1, E>(f);
   }
 }
+
+// Stores a wavefront's 32-row output tile whose lane l holds, per MFMA
+// d-tile t and j = 0..3, the 4 values of row l % 32 at d = 32 t + 8 j +
+// 4 (l / 32) .. +3 (the 32x32 accumulator layout): through the wavefront's
+// LDS area `tile` (32 x D values of GT; the caller has made it free), the
+// 16-byte chunk c of row r placed at chunk c ^ (r % 16) of the row, then
+// read back and stored a whole row per D sizeof(GT) / 16 lanes.  A store
+// straight from the accumulators writes 32 scattered pieces per
+// instruction, which held a workgroup ~2 us longer on its CU.  vals(t, j)
+// returns the lane's 4 values; rows r < rows_valid are stored at
+// dst + r * D.  The lane-dependent offsets are formed here, behind an empty
+// asm, so they are not hoisted into (and kept live through) a caller's loop.
+template <int D, typename GT, typename F>
+DEVI void store_tile_rows(char* tile, GT* dst, int rows_valid, F&& vals) {
+  constexpr int ES = (int)sizeof(GT);
+  constexpr int RB = D * ES;            // bytes per row
+  constexpr int CPR = RB / 16;          // 16-byte chunks per row
+  constexpr int MASK = (CPR < 16 ? CPR : 16) - 1;
+  constexpr int RPI = 64 / CPR;         // rows per store
+  static_assert(ES == 2 || ES == 4, "bf16 or fp32 rows");
+  const int ln = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int lr = ln & 31, hg = ln >> 5;
+  // write of (t, j): bf16: chunk 4 t + j, bytes 8 hg of it; fp32: chunk
+  // 8 t + 2 j + hg, all 16 bytes
+  int wa = lr * RB + (ES == 2 ? ((lr & MASK) << 4) + 8 * hg : (((lr & MASK) ^ hg) << 4));
+  int ra = (ln / CPR) * RB + (((ln % CPR) ^ ((ln / CPR) & MASK)) << 4);
+  int sa = (ln / CPR) * D + (ln % CPR) * (16 / ES);
+  asm volatile("" : "+v"(wa), "+v"(ra), "+v"(sa));
+#pragma unroll
+  for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 x = vals(t, j);
+      if constexpr (ES == 2)
+        *reinterpret_cast<u32x2*>(tile + (wa ^ ((4 * t + j) << 4))) =
+            u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+      else
+        *reinterpret_cast<f32x4*>(tile + (wa ^ ((8 * t + 2 * j) << 4))) = x;
+    }
+#pragma unroll
+  for (int kk = 0; kk < 32 / RPI; ++kk) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(
+        tile + (ra ^ (((kk * RPI) & MASK) << 4)) + kk * RPI * RB);
+    if (kk * RPI + ln / CPR < rows_valid)
+      *reinterpret_cast<u32x4*>(dst + kk * RPI * D + sa) = v;
+  }
+}

@@ -368,39 +368,31 @@ __device__ __forceinline__ void fa2_bwd_dkdv(
     exchange(dv_acc);
     if constexpr (GRP == 1) return;
   }
-  // ---- dK = scale * dK^T, dV = dV^T, lane = key, 16 d values per tile -------
+  // ---- dK = scale * dK^T, dV = dV^T (rows = this wavefront's 32 keys),
+  //      through LDS a whole row per store: no LDS read follows the walk's
+  //      last barrier (or, with two groups, the exchange's), so each
+  //      wavefront's area is free ----
+  static_assert(sizeof(DkdvSmem<D>) >= 4 * 32 * D * sizeof(float), "tiles fit the LDS block");
+  char* etile = reinterpret_cast<char*>(smg) + wave * (32 * D * (int)sizeof(float));
   if (hsplit > 1) {  // fp32 sums of this workgroup's heads
-    if (mykey < nk) {
-      const long n_kvh = total_blocks / num_n_blocks / hsplit;
-      float* pk = part + (((long)hs * n_kvh + kvh) * nk + mykey) * D;
-      float* pv = pk + (long)hsplit * n_kvh * nk * D;
-#pragma unroll
-      for (int t = 0; t < DT; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int d = 32 * t + 8 * j + 4 * g;
-          *reinterpret_cast<f32x4*>(pk + d) =
-              f32x4{dk_acc[t][4 * j], dk_acc[t][4 * j + 1], dk_acc[t][4 * j + 2], dk_acc[t][4 * j + 3]};
-          *reinterpret_cast<f32x4*>(pv + d) =
-              f32x4{dv_acc[t][4 * j], dv_acc[t][4 * j + 1], dv_acc[t][4 * j + 2], dv_acc[t][4 * j + 3]};
-        }
-    }
+    const long n_kvh = total_blocks / num_n_blocks / hsplit;
+    float* pk = part + (((long)hs * n_kvh + kvh) * nk + kw0) * D;
+    float* pv = pk + (long)hsplit * n_kvh * nk * D;
+    store_tile_rows<D, float>(etile, pk, nk - kw0, [&](int t, int j) {
+      return f32x4{dk_acc[t][4 * j], dk_acc[t][4 * j + 1], dk_acc[t][4 * j + 2], dk_acc[t][4 * j + 3]};
+    });
+    store_tile_rows<D, float>(etile, pv, nk - kw0, [&](int t, int j) {
+      return f32x4{dv_acc[t][4 * j], dv_acc[t][4 * j + 1], dv_acc[t][4 * j + 2], dv_acc[t][4 * j + 3]};
+    });
     return;
   }
-  if (mykey < nk) {
-    GT* dkr = dk + ((long)kvh * nk + mykey) * D;
-    GT* dvr = dv + ((long)kvh * nk + mykey) * D;
-#pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int d = 32 * t + 8 * j + 4 * g;
-        store4(dkr + d, dk_acc[t][4 * j] * scale, dk_acc[t][4 * j + 1] * scale,
-               dk_acc[t][4 * j + 2] * scale, dk_acc[t][4 * j + 3] * scale);
-        store4(dvr + d, dv_acc[t][4 * j], dv_acc[t][4 * j + 1], dv_acc[t][4 * j + 2],
-               dv_acc[t][4 * j + 3]);
-      }
-  }
+  store_tile_rows<D, GT>(etile, dk + ((long)kvh * nk + kw0) * D, nk - kw0, [&](int t, int j) {
+    return f32x4{dk_acc[t][4 * j] * scale, dk_acc[t][4 * j + 1] * scale,
+                 dk_acc[t][4 * j + 2] * scale, dk_acc[t][4 * j + 3] * scale};
+  });
+  store_tile_rows<D, GT>(etile, dv + ((long)kvh * nk + kw0) * D, nk - kw0, [&](int t, int j) {
+    return f32x4{dv_acc[t][4 * j], dv_acc[t][4 * j + 1], dv_acc[t][4 * j + 2], dv_acc[t][4 * j + 3]};
+  });
 }
 
 // dK = scale * sum of the hsplit partial dK^T, dV = sum of the dV^T, in
@@ -773,17 +765,17 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
     }
   }
 
-  if (qok) {
-    GT* dqr = dq + ((long)bhq * nq + qrow) * D;
-#pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int d = 32 * t + 8 * j + 4 * g;
-        store4(dqr + d, acc[t][4 * j] * scale, acc[t][4 * j + 1] * scale,
-               acc[t][4 * j + 2] * scale, acc[t][4 * j + 3] * scale);
-      }
-  }
+  // dQ rows through LDS (the K/V buffers: every wavefront's last product has
+  // read them once all have passed this barrier), stored whole rows at a time
+  static_assert(sizeof(DqSmem<D>) >= 4 * 32 * D * sizeof(GT), "dQ tiles fit the K/V buffers");
+  __builtin_amdgcn_s_waitcnt(kVmWaitLgkm0<63>());
+  barrier_only();
+  (void)qok;
+  store_tile_rows<D, GT>(reinterpret_cast<char*>(&sm) + wave * (32 * D * (int)sizeof(GT)),
+                         dq + ((long)bhq * nq + wrow0) * D, nq - wrow0, [&](int t, int j) {
+                           return f32x4{acc[t][4 * j] * scale, acc[t][4 * j + 1] * scale,
+                                        acc[t][4 * j + 2] * scale, acc[t][4 * j + 3] * scale};
+                         });
 }
 
 }  // namespace
