@@ -137,8 +137,8 @@ int teeny_flash_attn2_bwd(const void* q, const void* k, const void* v, const voi
                           size_t workspace_bytes, hipStream_t stream);
 
 /* Workspace the backward needs.  bf16: per (b, q head) and block of 32 query
- * rows, 32 values of LSE*log2(e) followed by 32 of Delta = rowsum(O * dO),
- * fp32, the last block padded; fp32: Delta [B*Hq, n_ctx_q].
+ * rows, 32 values of -LSE/softmax_scale followed by 32 of -Delta (Delta =
+ * rowsum(O * dO)), fp32, the last block padded; fp32: Delta [B*Hq, n_ctx_q].
  * No counterpart in the reference
  * (its executor sizes caches from RuntimeOp::param_shapes, flash_attn2.rs:449-457). */
 size_t teeny_flash_attn2_bwd_workspace_bytes(int n_ctx_q, int batch, int n_heads_q, int head_dim,

@@ -305,8 +305,8 @@ int fa2_fwd(bool causal, const void* q, const void* k, const void* v, void* o, f
   return launch(name, dim3((n_ctx_q + 63) / 64, batch * hq), dim3(64), 0, stream, args);
 }
 
-// bf16: per (b, q head) and block of 32 query rows, 32 values of LSE*log2(e)
-// then 32 of Delta (fp32; the last block padded).  fp32: Delta [B*Hq, n_ctx_q].
+// bf16: per (b, q head) and block of 32 query rows, 32 values of -LSE/scale
+// then 32 of -Delta (fp32; the last block padded).  fp32: Delta [B*Hq, n_ctx_q].
 constexpr int kLdRows = 32;
 size_t fa2_bwd_ws(int n_ctx_q, int batch, int hq, int head_dim, int dtype) {
   (void)head_dim;

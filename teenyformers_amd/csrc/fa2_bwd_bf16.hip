@@ -51,8 +51,11 @@ __device__ inline void store4(float* p, float a, float b, float c, float d) {
 
 
 // Per (b, q head) and block of BM query rows, ld holds BM values of
-// LSE * log2(e) followed by BM values of Delta = rowsum(O o dO), fp32; rows
-// past nq hold +inf and 0.  The dQ kernel writes it, the dK/dV kernel reads it.
+// -LSE / scale followed by BM values of -Delta (Delta = rowsum(O o dO)),
+// fp32; rows past nq hold -inf and 0.  The dQ kernel writes it, the dK/dV
+// kernel starts its score and dP accumulators from them, so that
+// S' = S - LSE / scale gives P = exp2(scale log2(e) S') and dP' = dP - Delta
+// gives dS = P dP' with no per-row value read while the products run.
 
 // ===========================================================================
 // dK / dV (key-parallel)
@@ -162,9 +165,15 @@ __device__ __forceinline__ void fa2_bwd_dkdv(
       dma16(qr, qdst + i * 4096, src + i * 4096, row0 * D * 2);
       dma16(dr, ddst + i * 4096, src + i * 4096, row0 * D * 2);
     }
-    if (wave == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(lr, (lds_void*)sm.ld[buf], 4, lane * 4,
+    if (wave == 0) {
+      // the lane offset formed here (volatile: not hoisted out of the walk):
+      // a value kept across the walk for this one load was spilled, and its
+      // reload waited for every load in flight
+      int ln;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(lr, (lds_void*)sm.ld[buf], 4, ln * 4,
                                                row0 * 2 * 4, 0, 0);
+    }
   };
 
   // ---- LDS read offsets (bytes) --------------------------------------------
@@ -218,19 +227,32 @@ __device__ __forceinline__ void fa2_bwd_dkdv(
     const char* dt = sm.d[buf];
     const float* lt = sm.ld[buf];
 
-    // ---- S = Q K^T (lane = key, 16 query rows); Q rows read KPF ahead ----
-    constexpr int KPF = 1;
-    f32x16 s = f32x16{}, dp = f32x16{};
+    // The row values of this lane's 16 query rows (row 8 j + 4 g + i for
+    // accumulator element 4 j + i) seed the score accumulator (-LSE / scale)
+    // and the dP accumulator (-Delta).
+    auto row_vals = [&](const float* p) {
+      const f32x4 c0 = *reinterpret_cast<const f32x4*>(p + 4 * g);
+      const f32x4 c1 = *reinterpret_cast<const f32x4*>(p + 8 + 4 * g);
+      const f32x4 c2 = *reinterpret_cast<const f32x4*>(p + 16 + 4 * g);
+      const f32x4 c3 = *reinterpret_cast<const f32x4*>(p + 24 + 4 * g);
+      return f32x16{c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3],
+                    c2[0], c2[1], c2[2], c2[3], c3[0], c3[1], c3[2], c3[3]};
+    };
+    // ---- S' = Q K^T - LSE / scale (lane = key, 16 query rows); Q rows read
+    //      KPF products ahead ----
+    constexpr int KPF = 2;
+    f32x16 s, dp;
     {
       u32x4 aq[DC];
 #pragma unroll
       for (int c = 0; c < KPF; ++c) aq[c] = *reinterpret_cast<const u32x4*>(qt + row_off[c]);
+      s = row_vals(lt);
 #pragma unroll
       for (int c = 0; c < DC; ++c) {
         if (c + KPF < DC) aq[c + KPF] = *reinterpret_cast<const u32x4*>(qt + row_off[c + KPF]);
         s = mfma32(as_bf16x8(aq[c]), kreg[c], s);
       }
-      sched_group(kDsRead, KPF);
+      sched_group(kDsRead, KPF + 4);
 #pragma unroll
       for (int c = 0; c < DC; ++c) {
         if (c + KPF < DC) sched_group(kDsRead, 1);
@@ -246,31 +268,31 @@ __device__ __forceinline__ void fa2_bwd_dkdv(
         if (mykey >= nk || (CAUSAL && mykey > qrow)) s[r] = -INFINITY;
       }
     }
-    // ---- dP = dO V^T on the matrix cores, P = exp2(S log2e scale - LSE
-    //      log2e) on the VALU; issue order fenced ----
+    // ---- dP' = dO V^T - Delta on the matrix cores, P = exp2(S' log2e
+    //      scale) on the VALU; issue order fenced ----
     uint32_t pb[8], dsb[8];
     {
       constexpr int PPC = 8 / DC;  // P pairs per product
+      constexpr int DPF = 2;       // dO / V rows read this many products ahead
       u32x4 ad[DC], av[DC];
 #pragma unroll
-      for (int c = 0; c < 1; ++c) {
+      for (int c = 0; c < DPF; ++c) {
         ad[c] = *reinterpret_cast<const u32x4*>(dt + row_off[c]);
         av[c] = *reinterpret_cast<const u32x4*>(vrows + row_off[c]);
       }
-      f32x4 l4;
+      dp = row_vals(lt + BM);
 #pragma unroll
       for (int c = 0; c < DC; ++c) {
-        if (c + 1 < DC) {
-          ad[c + 1] = *reinterpret_cast<const u32x4*>(dt + row_off[c + 1]);
-          av[c + 1] = *reinterpret_cast<const u32x4*>(vrows + row_off[c + 1]);
+        if (c + DPF < DC) {
+          ad[c + DPF] = *reinterpret_cast<const u32x4*>(dt + row_off[c + DPF]);
+          av[c + DPF] = *reinterpret_cast<const u32x4*>(vrows + row_off[c + DPF]);
         }
         dp = mfma32(as_bf16x8(ad[c]), as_bf16x8(av[c]), dp);
 #pragma unroll
         for (int i = 0; i < PPC; ++i) {
-          const int r = 2 * (c * PPC + i);  // registers r, r+1: rows 8(r/4) + 4g + r%4
-          if ((r & 3) == 0) l4 = *reinterpret_cast<const f32x4*>(lt + 8 * (r >> 2) + 4 * g);
-          const float p0 = fast_exp2(__builtin_fmaf(s[r], sl2, -l4[r & 3]));
-          const float p1 = fast_exp2(__builtin_fmaf(s[r + 1], sl2, -l4[(r & 3) + 1]));
+          const int r = 2 * (c * PPC + i);
+          const float p0 = fast_exp2(s[r] * sl2);
+          const float p1 = fast_exp2(s[r + 1] * sl2);
           s[r] = p0;
           s[r + 1] = p1;
           pb[r >> 1] = pack_bf16x2(p0, p1);
@@ -278,59 +300,57 @@ __device__ __forceinline__ void fa2_bwd_dkdv(
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // ---- dV^T += dO^T P on the matrix cores, dS = P (dP - Delta) on the
-    //      VALU (hh = 0 pairs after the first product, hh = 1 after ...);
-    //      then dK^T += Q^T dS ----
+    // ---- dV^T += dO^T P on the matrix cores, dS = P dP' on the VALU (hh = 0
+    //      pairs after the first product, hh = 1 after ...); then
+    //      dK^T += Q^T dS.  Transposed fragments read TPF products ahead ----
     {
       constexpr int NJ = 2 * DT;   // products of dV^T
       constexpr int PPJ = 8 / NJ;  // dS pairs per product
-      bf16x8 ta = tr_read(dt, 0, 0);
-      f32x4 d4;
+      constexpr int TPF = 2;
+      bf16x8 ta[NJ];
       uint32_t plo[4], dslo[PRECISE ? 8 : 1];
+#pragma unroll
+      for (int j = 0; j < TPF; ++j) ta[j] = tr_read(dt, j / DT, j % DT);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int hh = j / DT, t = j % DT;
-        bf16x8 tn;
-        if (j + 1 < NJ) tn = tr_read(dt, (j + 1) / DT, (j + 1) % DT);
-        dv_acc[t] = mfma32(ta, as_bf16x8(u32x4{pb[4 * hh], pb[4 * hh + 1], pb[4 * hh + 2],
-                                                 pb[4 * hh + 3]}), dv_acc[t]);
+        if (j + TPF < NJ) ta[j + TPF] = tr_read(dt, (j + TPF) / DT, (j + TPF) % DT);
+        dv_acc[t] = mfma32(ta[j], as_bf16x8(u32x4{pb[4 * hh], pb[4 * hh + 1], pb[4 * hh + 2],
+                                                    pb[4 * hh + 3]}), dv_acc[t]);
         if constexpr (PRECISE) {
           if (t == 0)  // the low parts of this half's P (fp32 P is still in s)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
               plo[i] = pack_bf16x2(s[8 * hh + 2 * i] - bf16lo(pb[4 * hh + i]),
                                    s[8 * hh + 2 * i + 1] - bf16hi(pb[4 * hh + i]));
-          dv_acc[t] = mfma32(ta, as_bf16x8(u32x4{plo[0], plo[1], plo[2], plo[3]}), dv_acc[t]);
+          dv_acc[t] = mfma32(ta[j], as_bf16x8(u32x4{plo[0], plo[1], plo[2], plo[3]}), dv_acc[t]);
         }
 #pragma unroll
         for (int i = 0; i < PPJ; ++i) {
           const int r = 2 * (j * PPJ + i);
-          if ((r & 3) == 0) d4 = *reinterpret_cast<const f32x4*>(lt + BM + 8 * (r >> 2) + 4 * g);
           if constexpr (PRECISE) {
-            const float ds0 = s[r] * (dp[r] - d4[r & 3]);
-            const float ds1 = s[r + 1] * (dp[r + 1] - d4[(r & 3) + 1]);
+            const float ds0 = s[r] * dp[r];
+            const float ds1 = s[r + 1] * dp[r + 1];
             dsb[r >> 1] = pack_bf16x2(ds0, ds1);
             dslo[r >> 1] = pack_bf16x2(ds0 - bf16lo(dsb[r >> 1]), ds1 - bf16hi(dsb[r >> 1]));
           } else {
-            dsb[r >> 1] = pack_bf16x2(s[r] * (dp[r] - d4[r & 3]),
-                                      s[r + 1] * (dp[r + 1] - d4[(r & 3) + 1]));
+            dsb[r >> 1] = pack_bf16x2(s[r] * dp[r], s[r + 1] * dp[r + 1]);
           }
         }
-        if (j + 1 < NJ) ta = tn;
         __builtin_amdgcn_sched_barrier(0);
       }
-      ta = tr_read(qt, 0, 0);
+#pragma unroll
+      for (int j = 0; j < TPF; ++j) ta[j] = tr_read(qt, j / DT, j % DT);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const int hh = j / DT, t = j % DT;
-        bf16x8 tn;
-        if (j + 1 < NJ) tn = tr_read(qt, (j + 1) / DT, (j + 1) % DT);
-        dk_acc[t] = mfma32(ta, as_bf16x8(u32x4{dsb[4 * hh], dsb[4 * hh + 1], dsb[4 * hh + 2],
-                                                  dsb[4 * hh + 3]}), dk_acc[t]);
+        if (j + TPF < NJ) ta[j + TPF] = tr_read(qt, (j + TPF) / DT, (j + TPF) % DT);
+        dk_acc[t] = mfma32(ta[j], as_bf16x8(u32x4{dsb[4 * hh], dsb[4 * hh + 1], dsb[4 * hh + 2],
+                                                     dsb[4 * hh + 3]}), dk_acc[t]);
         if constexpr (PRECISE)
-          dk_acc[t] = mfma32(ta, as_bf16x8(u32x4{dslo[4 * hh], dslo[4 * hh + 1], dslo[4 * hh + 2],
-                                                    dslo[4 * hh + 3]}), dk_acc[t]);
-        if (j + 1 < NJ) ta = tn;
+          dk_acc[t] = mfma32(ta[j], as_bf16x8(u32x4{dslo[4 * hh], dslo[4 * hh + 1], dslo[4 * hh + 2],
+                                                       dslo[4 * hh + 3]}), dk_acc[t]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     head = nhead;
@@ -504,8 +524,9 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   }
   // LSE * log2(e) and Delta = rowsum(O o dO) of this row (rows past nq: +inf
   // and 0): the lane holds half of the row's d values (8 g + 16 c ..), the
-  // other half is in lane l ^ 32.  Written to ld for the dK/dV kernel, which
-  // runs after this one.
+  // other half is in lane l ^ 32.  For the dK/dV kernel, which runs after
+  // this one, ld gets -LSE / scale and -Delta: the initial values of its
+  // score and dP accumulators.
   float lse2 = INFINITY, dlt = 0.0f;
   {
     const long row = (long)bhq * nq + min(qrow, nq - 1);
@@ -532,8 +553,8 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
     const int nq_pad = (nq + BM - 1) / BM * BM;  // ld rows: whole blocks of BM
     if (g == 0 && qrow < nq_pad) {
       float* blk = ld + ((long)bhq * nq_pad + qrow) / BM * (2 * BM);
-      blk[qrow % BM] = lse2;
-      blk[BM + qrow % BM] = dlt;
+      blk[qrow % BM] = qok ? -lse[(long)bhq * nq + qrow] / scale : -INFINITY;
+      blk[BM + qrow % BM] = -dlt;
     }
   }
   const float sl2 = scale * kLog2e;
