@@ -394,8 +394,8 @@ int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void
     float* ld = (float*)workspace;
     // dQ first: one workgroup per 128 query rows of a (b, q head), or, for
     // causal GQA groups of 4, per (b, kv head, 32 rows) with a wavefront per
-    // q head as in the forward; it also writes LSE * log2(e) and Delta of
-    // its rows to ld for the dK/dV kernel
+    // q head as in the forward; it also writes -LSE/scale and -Delta of its
+    // rows to ld for the dK/dV kernel
     const bool pack = causal && hq == 4 * hkv;
     int nmb = pack ? (n_ctx_q + 31) / 32 : (n_ctx_q + 127) / 128;
     long total = (long)nmb * batch * (pack ? hkv : hq);
