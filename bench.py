@@ -426,7 +426,7 @@ def bench_llama_block(torch):
                             rope_base=5e5, intermediate_size=8192, n_kv_heads_=8)
     w = llama.init_weights(cfg, dtype=torch.bfloat16, seed=11)
     x = torch.randn((4, 2048, 2048), device="cuda").to(torch.bfloat16)
-    ms = _time(torch, lambda: llama.block_forward(cfg, w, x), 10)
+    ms = _time(torch, lambda: llama.block_forward(cfg, w, x), 50)
     f = llama.prefill_flops(cfg, 4, 2048) - 2.0 * 2048 * 32 * 4  # no lm_head
     return {"ms": round(ms, 3), "tflops": round(f / ms / 1e9, 1),
             "pct_peak": round(f / ms / 1e9 / PEAK_BF16_TFLOPS, 4), "flop": f}

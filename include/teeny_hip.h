@@ -116,6 +116,17 @@ int teeny_flash_attn2_fwd(const void* q, const void* k, const void* v, void* o, 
                           int batch, int n_heads_q, int n_heads_kv, int head_dim, int dtype,
                           hipStream_t stream);
 
+/* The forward (causal or not) with MergeHeadsOp fused: o is written as
+ * [B, n_ctx_q, n_heads_q * head_dim], the layout teeny_merge_heads makes of
+ * the forward's [B, Hq, n_ctx_q, D] (the reference records the two ops one
+ * after the other, src/layers/attention.rs:132-143); the same kernels, the
+ * same output bits, one launch and one pass over O fewer.  l is [B*Hq,
+ * n_ctx_q] as above.  bf16 only (TEENY_ERR_UNSUPPORTED otherwise). */
+int teeny_flash_attn2_fwd_merged(const void* q, const void* k, const void* v, void* o, float* l,
+                                 int n_ctx_q, int n_ctx_k, float softmax_scale, float neg_inf,
+                                 int batch, int n_heads_q, int n_heads_kv, int head_dim,
+                                 int dtype, int causal, hipStream_t stream);
+
 /* Replaces CausalFlashAttn2RuntimeOp::pack_backward_args + launch
  * (flash_attn2.rs:493-529): (q, k, v, o, do, l, dq, dk, dv, n_ctx_q, n_ctx_k,
  * softmax_scale).  dq, dk and dv are overwritten: unlike the reference

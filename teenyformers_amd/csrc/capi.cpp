@@ -266,7 +266,7 @@ bool scale_ok(float scale, int dtype) {
 
 int fa2_fwd(bool causal, const void* q, const void* k, const void* v, void* o, float* l,
             int n_ctx_q, int n_ctx_k, float scale, float neg_inf, int batch, int hq, int hkv,
-            int head_dim, int dtype, hipStream_t stream) {
+            int head_dim, int dtype, hipStream_t stream, int o_merged = 0) {
   int rc = fa2_check(q, k, v, n_ctx_q, n_ctx_k, batch, hq, hkv, head_dim, dtype);
   if (rc) return rc;
   if (!o || !l) return TEENY_ERR_NULL_POINTER;
@@ -296,10 +296,12 @@ int fa2_fwd(bool causal, const void* q, const void* k, const void* v, void* o, f
     int tot = (int)total;
     snprintf(name, sizeof name, "teeny_fa2_fwd_bf16_d%d_%s%s", head_dim, cz,
              pack == 4 ? "_g4" : pack == 8 ? "_g8" : w8 ? "_w8" : "");
-    void* args[] = {&q, &k, &v, &o, &l, &n_ctx_q, &n_ctx_k, &scale, &hq, &hkv, &nmb, &tot};
+    void* args[] = {&q, &k, &v, &o, &l, &n_ctx_q, &n_ctx_k, &scale, &hq, &hkv, &nmb, &tot,
+                    &o_merged};
     const int threads = pack ? 64 * pack : 2 * bm;
     return launch(name, dim3(tot), dim3(threads), 0, stream, args);
   }
+  if (o_merged) return TEENY_ERR_UNSUPPORTED;
   snprintf(name, sizeof name, "teeny_fa2_fwd_f32_d%d_%s", head_dim, cz);
   void* args[] = {&q, &k, &v, &o, &l, &n_ctx_q, &n_ctx_k, &scale, &hq, &hkv};
   return launch(name, dim3((n_ctx_q + 63) / 64, batch * hq), dim3(64), 0, stream, args);
@@ -569,6 +571,15 @@ int teeny_flash_attn2_fwd(const void* q, const void* k, const void* v, void* o, 
                           hipStream_t stream) {
   return fa2_fwd(false, q, k, v, o, l, n_ctx_q, n_ctx_k, softmax_scale, neg_inf, batch,
                  n_heads_q, n_heads_kv, head_dim, dtype, stream);
+}
+
+int teeny_flash_attn2_fwd_merged(const void* q, const void* k, const void* v, void* o, float* l,
+                                 int n_ctx_q, int n_ctx_k, float softmax_scale, float neg_inf,
+                                 int batch, int n_heads_q, int n_heads_kv, int head_dim,
+                                 int dtype, int causal, hipStream_t stream) {
+  if (dtype != TEENY_BF16) return TEENY_ERR_UNSUPPORTED;  // the bf16 kernels only
+  return fa2_fwd(causal != 0, q, k, v, o, l, n_ctx_q, n_ctx_k, softmax_scale, neg_inf, batch,
+                 n_heads_q, n_heads_kv, head_dim, dtype, stream, 1);
 }
 
 int teeny_causal_flash_attn2_bwd(const void* q, const void* k, const void* v, const void* o,

@@ -71,7 +71,7 @@ template <int D, bool CAUSAL, int NW = 4, bool PACK = false, int NSUB = 2>
 __device__ __forceinline__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict__ k,
                              const bf16* __restrict__ v, bf16* __restrict__ o,
                              float* __restrict__ lse, int nq, int nk, float scale, int hq, int hkv,
-                             int num_m_blocks, int total_blocks) {
+                             int num_m_blocks, int total_blocks, int o_merged) {
   constexpr int BN = SUBN * NSUB;      // keys per tile
   constexpr int BM = 32 * NW;          // query rows per workgroup
   constexpr int NT = 64 * NW;          // threads
@@ -487,7 +487,10 @@ __device__ __forceinline__ void fa2_fwd_bf16(const bf16* __restrict__ q, const b
   const int lr = ln & 31;
   int wa = lr * (2 * D) + 8 * (ln >> 5) + ((lr & (CPR - 1)) << 4);
   int ra = (ln / CPR) * (2 * D) + (((ln % CPR) ^ (ln / CPR)) << 4);
-  int sa = (ln / CPR) * D + 8 * (ln % CPR);  // element offset of the lane's store
+  // O's layout: [B, Hq, Sq, D] (rows of a head D apart), or, o_merged,
+  // [B, Sq, Hq, D], the merged-heads layout (rows Hq D apart)
+  const int rs = o_merged ? hq * D : D;
+  int sa = (ln / CPR) * rs + 8 * (ln % CPR);  // element offset of the lane's store
   asm volatile("" : "+v"(wa), "+v"(ra), "+v"(sa));
 #pragma unroll
   for (int t = 0; t < DT; ++t) {
@@ -499,13 +502,14 @@ __device__ __forceinline__ void fa2_fwd_bf16(const bf16* __restrict__ q, const b
       *reinterpret_cast<u32x2*>(ot + (wa ^ ((4 * t + j) << 4))) = w;
     }
   }
-  bf16* ob = o + ((long)bhq * nq + wrow0) * D;
+  const int hd = bhq % hq;  // this wavefront's q head within its batch row
+  bf16* ob = o + (long)(bhq - hd) * nq * D + (long)wrow0 * rs + (long)hd * (o_merged ? D : nq * D);
 #pragma unroll
   for (int kk = 0; kk < 32 / RPI; ++kk) {
     const u32x4 val = *reinterpret_cast<const u32x4*>(
         ot + (ra ^ (((kk % (CPR / RPI)) * RPI) << 4)) + kk * RPI * 2 * D);
     if (wrow0 + kk * RPI + ln / CPR < nq)
-      *reinterpret_cast<u32x4*>(ob + kk * RPI * D + sa) = val;
+      *reinterpret_cast<u32x4*>(ob + kk * RPI * rs + sa) = val;
   }
   if (qrow < nq && g == 0) lse[(long)bhq * nq + qrow] = (m_run + __log2f(l_tot)) * kLn2;
 }
@@ -524,8 +528,9 @@ __device__ __forceinline__ void fa2_fwd_bf16(const bf16* __restrict__ q, const b
   extern "C" __global__ __launch_bounds__(64 * NW)                                               \
       __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void teeny_fa2_fwd_bf16_d##D##_##SFX(       \
           const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,        \
-          float scale, int hq, int hkv, int nmb, int total) {                                    \
-    fa2_fwd_bf16<D, C, NW, PACK, NSUB>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total);       \
+          float scale, int hq, int hkv, int nmb, int total, int o_merged) {                      \
+    fa2_fwd_bf16<D, C, NW, PACK, NSUB>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total,        \
+                                       o_merged);                                                \
   }
 
 // 4 wavefronts, 128 query rows of one (b, q head) per workgroup

@@ -237,7 +237,12 @@ class Llama:
         else:
             if pos0 != 0:
                 raise ValueError("prefill must start at position 0")
-            # causal FA2 over the cache: keys past S are masked (key > query)
+            # causal FA2 over the cache: keys past S are masked (key > query);
+            # bf16 writes the merged-heads layout itself (one launch, one pass
+            # over O fewer than the forward and then merge_heads)
+            if q.dtype == torch.bfloat16:
+                att, _ = ops.flash_attn2_fwd_merged(q, cache.k[i], cache.v[i], scale, causal=True)
+                return ops.linear_split(att, self._lw(p + "o_proj.weight"))
             o, _ = ops.flash_attn2_fwd(q, cache.k[i], cache.v[i], scale, causal=True)
         # one position: [B, Hq, 1, D] is already the merged [B, 1, Hq D] layout
         att = o.view(B, S, Hq * D) if S == 1 else ops.merge_heads(o)

@@ -85,6 +85,26 @@ def flash_attn2_fwd(q, k, v, softmax_scale: float | None = None, causal: bool = 
     return out, lse
 
 
+def flash_attn2_fwd_merged(q, k, v, softmax_scale: float | None = None, causal: bool = True):
+    """The forward with the heads merged (MergeHeadsOp fused): o [B, Sq, Hq*D]
+    (merge_heads of flash_attn2_fwd's o, bit for bit) and lse [B, Hq, Sq].
+    bf16 q [B, Hq, Sq, D], k/v [B, Hkv, Sk, D]."""
+    q4, k4, v4 = _as4(q), _as4(k), _as4(v)
+    _dev(q4, k4, v4)
+    B, Hq, Sq, D = q4.shape
+    Hkv, Sk = k4.shape[1], k4.shape[2]
+    if k4.shape != v4.shape or k4.shape[0] != B or k4.shape[3] != D:
+        raise ValueError("k and v must be [B, Hkv, Sk, D] matching q")
+    if not (q4.dtype == k4.dtype == v4.dtype == torch.bfloat16):
+        raise TypeError("flash_attn2_fwd_merged: bf16 q, k, v")
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    out = torch.empty((B, Sq, Hq * D), dtype=q4.dtype, device=q4.device)
+    lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q4.device)
+    call("teeny_flash_attn2_fwd_merged", _p(q4), _p(k4), _p(v4), _p(out), _p(lse), Sq, Sk, scale,
+         float("-inf"), B, Hq, Hkv, D, _code(q4), int(bool(causal)), _stream())
+    return out, lse
+
+
 def flash_attn2_bwd_workspace_bytes(q: torch.Tensor, k: torch.Tensor | None = None) -> int:
     """Backward workspace; given k, the size that also allows the GQA head
     split of the dK/dV kernel where it applies."""

@@ -53,6 +53,20 @@ def test_fa2_fwd_validation(L):
     assert fwd(L, scale=float("nan")) == VALUE
 
 
+def test_fa2_fwd_merged_validation(L):
+    """The merged-heads forward validates like the forward and is bf16 only."""
+    def m(causal=1, **kw):
+        a = dict(q=P, nq=128, scale=0.125, dtype=BF16)
+        a.update(kw)
+        return L.teeny_flash_attn2_fwd_merged(a["q"], P, P, P, P, a["nq"], 128, a["scale"],
+                                              NEG_INF, 1, 4, 4, 64, a["dtype"], causal, None)
+    for c in (0, 1):
+        assert m(c, dtype=F32) == UNSUP
+        assert m(c, q=None) == NULLP
+        assert m(c, nq=0) == SHAPE
+        assert m(c, scale=0.0) == VALUE
+
+
 def test_fa2_scale_domain(L):
     """bf16 kernels fold the scale into the exponent after masking raw
     scores to -inf: scale must be > 0 there (0 or negative would turn masked

@@ -175,6 +175,38 @@ def test_fa2_bf16_fwd(cuda, shape, causal):
     assert np.abs(host(lse) - le).max() <= 2e-2
 
 
+MERGED_SHAPES = BF16_SHAPES + [
+    (16, 32, 8, 512, 512, 128),    # the Llama-3-8B prefill's attention
+    (1, 8, 8, 2048, 2048, 128),    # plain, several row blocks
+    (1, 8, 2, 5000, 5000, 128),    # GQA 4 packed, long
+]
+
+
+@pytest.mark.parametrize("shape", MERGED_SHAPES)
+@pytest.mark.parametrize("causal", [True, False])
+def test_fa2_bf16_fwd_merged(cuda, shape, causal):
+    """The merged-heads forward writes [B, Sq, Hq*D]: bit for bit
+    merge_heads of the [B, Hq, Sq, D] forward, LSE bit for bit the same."""
+    B, Hq, Hkv, Sq, Sk, D = shape
+    g = torch.Generator(device="cuda").manual_seed(Sq * 7 + Hq)
+    q = torch.randn((B, Hq, Sq, D), generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn((B, Hkv, Sk, D), generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn((B, Hkv, Sk, D), generator=g, device="cuda").to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = ops.flash_attn2_fwd(q, k, v, scale, causal)
+    om, lm = ops.flash_attn2_fwd_merged(q, k, v, scale, causal)
+    torch.cuda.synchronize()
+    assert om.shape == (B, Sq, Hq * D)
+    assert torch.equal(om.view(torch.int16), ops.merge_heads(o).view(torch.int16))
+    assert torch.equal(lm.view(torch.int32), lse.view(torch.int32))
+
+
+def test_fa2_fwd_merged_rejects_f32(cuda):
+    q = torch.zeros((1, 2, 8, 64), device="cuda")
+    with pytest.raises(TypeError):
+        ops.flash_attn2_fwd_merged(q, q, q)
+
+
 @pytest.mark.parametrize("B,Hq,Hkv,S,D", [(1, 8, 2, 8300, 64), (1, 8, 2, 5000, 128)])
 def test_fa2_bf16_fwd_packed_long(cuda, B, Hq, Hkv, S, D):
     """The GQA-packed causal forward (a wavefront per q head of a group of
