@@ -19,13 +19,18 @@
 // limit, measured), so a product never allocates device memory and products
 // on different streams or threads share nothing but the read-only plan.
 // Plans (descriptors and the heuristic's first algorithm) are built once per
-// (device, dtype, M, N, K) under a lock and never freed; the matmul itself is
-// enqueued outside the lock.  Under stream capture nothing is built or run
+// (device, dtype, M, N, K, ldy) under a lock and never freed; the matmul
+// itself is enqueued outside the lock.  Where the heuristic has no algorithm
+// for a wide product (the 128256-row lm_head at 8192 rows), the product runs
+// as column blocks of at most 32768 features (y's rows keep their stride),
+// each its own plan: the same sums per output, since no algorithm here splits
+// K.  Under stream capture nothing is built or run
 // here (the caller's own GEMM runs instead), so which GEMM a captured graph
 // holds does not depend on what ran before the capture.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <map>
 #include <mutex>
@@ -44,13 +49,13 @@ struct Device {
   bool tried = false;
   hipblasLtHandle_t handle = nullptr;
   // std::map: a plan's address stays valid while other plans are added
-  std::map<std::tuple<int, int, int, int>, Plan> plans;
+  std::map<std::tuple<int, int, int, int, int>, Plan> plans;
 };
 
 std::mutex mu;
 std::map<int, Device> devices;
 
-Plan make_plan(hipblasLtHandle_t h, hipDataType t, int M, int N, int K) {
+Plan make_plan(hipblasLtHandle_t h, hipDataType t, int M, int N, int K, int ldy) {
   Plan p;
   const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
   if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
@@ -59,7 +64,7 @@ Plan make_plan(hipblasLtHandle_t h, hipDataType t, int M, int N, int K) {
   hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb);
   if (hipblasLtMatrixLayoutCreate(&p.a, t, K, N, K) != HIPBLAS_STATUS_SUCCESS ||
       hipblasLtMatrixLayoutCreate(&p.b, t, K, M, K) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatrixLayoutCreate(&p.d, t, N, M, N) != HIPBLAS_STATUS_SUCCESS)
+      hipblasLtMatrixLayoutCreate(&p.d, t, N, M, ldy) != HIPBLAS_STATUS_SUCCESS)
     return p;
   hipblasLtMatmulPreference_t pref = nullptr;
   if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return p;
@@ -78,8 +83,20 @@ Plan make_plan(hipblasLtHandle_t h, hipDataType t, int M, int N, int K) {
   return p;
 }
 
+constexpr int kMaxBlocks = 8;
+constexpr int kBlockN = 32768;  // widest column block of a split product
+
+// the plan of (t, M, n, K) with y's row stride ldy, built on first use;
+// nullptr: no algorithm.  Called with mu held.
+const Plan* plan_of(Device& d, hipDataType t, int M, int n, int K, int ldy) {
+  auto key = std::make_tuple((int)t, M, n, K, ldy);
+  auto it = d.plans.find(key);
+  if (it == d.plans.end()) it = d.plans.emplace(key, make_plan(d.handle, t, M, n, K, ldy)).first;
+  return it->second.ok ? &it->second : nullptr;
+}
+
 // 0: y written (launched on `stream`); -1: hipBLASLt is not used for this
-// device, shape or stream state, nothing was launched.
+// device, shape or stream state, and y is left to the caller's own GEMM.
 int lt_gemm(hipDataType t, const void* x, const void* w, void* y, int M, int N, int K,
             hipStream_t stream) {
   int dev = 0;
@@ -88,7 +105,8 @@ int lt_gemm(hipDataType t, const void* x, const void* w, void* y, int M, int N, 
   if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
     return -1;
   hipblasLtHandle_t handle = nullptr;
-  const Plan* plan = nullptr;
+  const Plan* plans[kMaxBlocks] = {};
+  int nblk = 1, bn = N;
   {
     std::lock_guard<std::mutex> lock(mu);
     Device& d = devices[dev];
@@ -97,18 +115,32 @@ int lt_gemm(hipDataType t, const void* x, const void* w, void* y, int M, int N, 
       if (hipblasLtCreate(&d.handle) != HIPBLAS_STATUS_SUCCESS) d.handle = nullptr;
     }
     if (!d.handle) return -1;
-    auto key = std::make_tuple((int)t, M, N, K);
-    auto it = d.plans.find(key);
-    if (it == d.plans.end()) it = d.plans.emplace(key, make_plan(d.handle, t, M, N, K)).first;
-    if (!it->second.ok) return -1;
+    plans[0] = plan_of(d, t, M, N, K, N);
+    if (!plans[0]) {
+      // column blocks: equal widths (multiples of 64), the last one narrower
+      nblk = (N + kBlockN - 1) / kBlockN;
+      if (nblk < 2 || nblk > kMaxBlocks) return -1;
+      bn = ((N + nblk - 1) / nblk + 63) / 64 * 64;
+      nblk = (N + bn - 1) / bn;
+      for (int i = 0; i < nblk; ++i)
+        if (!(plans[i] = plan_of(d, t, M, std::min(bn, N - i * bn), K, N))) return -1;
+    }
     handle = d.handle;
-    plan = &it->second;
   }
+  const size_t esz = t == HIP_R_16BF ? 2 : 4;
   const float alpha = 1.0f, beta = 0.0f;
-  const hipblasStatus_t s = hipblasLtMatmul(handle, plan->desc, &alpha, w, plan->a, x, plan->b,
-                                            &beta, y, plan->d, y, plan->d, &plan->algo, nullptr,
-                                            0, stream);
-  return s == HIPBLAS_STATUS_SUCCESS ? 0 : -1;
+  for (int i = 0; i < nblk; ++i) {
+    const Plan* plan = plans[i];
+    const void* wi = static_cast<const char*>(w) + (size_t)i * bn * K * esz;
+    void* yi = static_cast<char*>(y) + (size_t)i * bn * esz;
+    const hipblasStatus_t s = hipblasLtMatmul(handle, plan->desc, &alpha, wi, plan->a, x,
+                                              plan->b, &beta, yi, plan->d, yi, plan->d,
+                                              &plan->algo, nullptr, 0, stream);
+    // after a failed block the caller's own GEMM rewrites the whole of y,
+    // in stream order after the blocks already enqueued
+    if (s != HIPBLAS_STATUS_SUCCESS) return -1;
+  }
+  return 0;
 }
 
 }  // namespace

@@ -74,6 +74,23 @@ def test_gemm_llama_shapes(cuda, M, N, K, entry):
     _check(y[rows].float().cpu().numpy(), x[rows], w)
 
 
+def test_linear_wide_column_blocks(cuda):
+    """The all-position lm_head (8192 x 128256 x 4096), for which hipBLASLt
+    has no single algorithm: teeny_linear_bf16 runs it as column blocks of
+    y.  Rows from three tiles against float64 products, and every output
+    bit-equal to the own GEMM's (the same sums per output)."""
+    M, N, K = 8192, 128256, 4096
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
+    w = (0.02 * torch.randn((N, K), generator=g, device="cuda")).to(torch.bfloat16)
+    y = _gemm(x, w)
+    rows = [*range(0, 32), *range(M // 2 + 3, M // 2 + 35), *range(M - 32, M)]
+    want = (x[rows].double() @ w.double().T)
+    bar = want.abs() * 2.0 ** -8 + 1e-6 * want.abs().max()
+    assert bool(((y[rows].double() - want).abs() <= bar).all())
+    assert torch.equal(y, _gemm(x, w, "teeny_gemm_bf16"))
+
+
 def test_gemm_linear_op(cuda):
     """ops.linear routes bf16 prompts to teeny_linear_bf16 (any leading shape)
     and still takes the decode kernels at 16 rows; ops.gemm_own is the own
