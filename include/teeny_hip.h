@@ -127,6 +127,31 @@ int teeny_flash_attn2_fwd_merged(const void* q, const void* k, const void* v, vo
                                  int batch, int n_heads_q, int n_heads_kv, int head_dim,
                                  int dtype, int causal, hipStream_t stream);
 
+/* The forward with its Q taken from the fused QKV projection and MergeHeadsOp
+ * fused (no counterpart in the reference, which records TransposeHeadsOp +
+ * RopeOp on Q, the attention op and MergeHeadsOp one after the other,
+ * src/layers/attention.rs:97-143): qkv [B, n_ctx_q, (Hq + 2 Hkv) * D] as
+ * teeny_qkv_rope_split takes it; the kernel rotates each q row r with the
+ * (cos, sin) of position r from rope_cs (teeny_rope_table over at least
+ * n_ctx_q positions rounded up to 32) as it loads it; k, v [B, Hkv, n_ctx_k,
+ * D] (the cache teeny_qkv_rope_split wrote, q_out NULL); o [B, n_ctx_q,
+ * Hq * D], l [B*Hq, n_ctx_q].  The same output bits as teeny_qkv_rope_split
+ * into a Q buffer then teeny_flash_attn2_fwd_merged, without Q's write and
+ * read.  bf16 only; rope_cs 16-byte aligned. */
+int teeny_flash_attn2_fwd_qkv(const void* qkv, const float* rope_cs, const void* k, const void* v,
+                              void* o, float* l, int n_ctx_q, int n_ctx_k, float softmax_scale,
+                              float neg_inf, int batch, int n_heads_q, int n_heads_kv,
+                              int head_dim, int dtype, int causal, hipStream_t stream);
+
+/* (cos, sin) of RoPE's interleaved pairs at positions 0 .. n_pos-1 (n_pos a
+ * multiple of 32, head_dim of 16): n_pos * head_dim fp32 values, theta =
+ * fp32(pos) * fp32(exp_f64(fp32(k) * (-2 ln_rope_base / head_dim)))
+ * (rope.rs:86-88), the values every rotating kernel here evaluates, in the
+ * order teeny_flash_attn2_fwd_qkv loads them: pair k = 8c + 4g + 2m + e of
+ * position p is floats 4 f + 2 e, +1 with f = ((p / 32) * (head_dim / 8) +
+ * 2c + m) * 64 + (p % 32) * 2 + g.  No counterpart in the reference. */
+int teeny_rope_table(float* cs, int n_pos, int head_dim, float ln_rope_base, hipStream_t stream);
+
 /* Replaces CausalFlashAttn2RuntimeOp::pack_backward_args + launch
  * (flash_attn2.rs:493-529): (q, k, v, o, do, l, dq, dk, dv, n_ctx_q, n_ctx_k,
  * softmax_scale).  dq, dk and dv are overwritten: unlike the reference
@@ -283,7 +308,9 @@ int teeny_token_embed_fwd(const void* ids, const void* weight, void* out, int se
  *   and K (with RoPE) / V written into caches [B, Hkv, cache_len, D] at rows
  *   pos0 .. pos0+seq_len-1; RoPE positions are absolute (pos0 + s).  Fuses
  *   the reference's TransposeHeadsOp x3 + RopeOp x2 (src/layers/attention.rs:97-123)
- *   with their arithmetic (transpose_heads.rs:65-67, rope.rs:86-96).
+ *   with their arithmetic (transpose_heads.rs:65-67, rope.rs:86-96).  q_out
+ *   may be NULL: then only the cache rows are written (the prompt attention
+ *   teeny_flash_attn2_fwd_qkv reads and rotates Q itself).
  * teeny_decode_attention: one query row per (b, q head), q [B, Hq, D],
  *   against cache rows 0 .. n_keys-1 (all visible: the newest query is the
  *   last position), o [B, Hq, D].  Split over the keys; workspace of

@@ -46,6 +46,8 @@ _SIGNATURES = {
     "teeny_causal_flash_attn2_fwd": ([_p] * 5 + [_i, _i, _f, _f, _i, _i, _i, _i, _i, _p], _i),
     "teeny_flash_attn2_fwd": ([_p] * 5 + [_i, _i, _f, _f, _i, _i, _i, _i, _i, _p], _i),
     "teeny_flash_attn2_fwd_merged": ([_p] * 5 + [_i, _i, _f, _f, _i, _i, _i, _i, _i, _i, _p], _i),
+    "teeny_flash_attn2_fwd_qkv": ([_p] * 6 + [_i, _i, _f, _f, _i, _i, _i, _i, _i, _i, _p], _i),
+    "teeny_rope_table": ([_p, _i, _i, _f, _p], _i),
     "teeny_causal_flash_attn2_bwd": ([_p] * 9 + [_i, _i, _f, _i, _i, _i, _i, _i, _p, _sz, _p], _i),
     "teeny_flash_attn2_bwd": ([_p] * 9 + [_i, _i, _f, _i, _i, _i, _i, _i, _p, _sz, _p], _i),
     "teeny_flash_attn2_bwd_workspace_bytes": ([_i, _i, _i, _i, _i], _sz),

@@ -266,7 +266,8 @@ bool scale_ok(float scale, int dtype) {
 
 int fa2_fwd(bool causal, const void* q, const void* k, const void* v, void* o, float* l,
             int n_ctx_q, int n_ctx_k, float scale, float neg_inf, int batch, int hq, int hkv,
-            int head_dim, int dtype, hipStream_t stream, int o_merged = 0) {
+            int head_dim, int dtype, hipStream_t stream, int o_merged = 0,
+            const float* rope_cs = nullptr) {
   int rc = fa2_check(q, k, v, n_ctx_q, n_ctx_k, batch, hq, hkv, head_dim, dtype);
   if (rc) return rc;
   if (!o || !l) return TEENY_ERR_NULL_POINTER;
@@ -297,11 +298,11 @@ int fa2_fwd(bool causal, const void* q, const void* k, const void* v, void* o, f
     snprintf(name, sizeof name, "teeny_fa2_fwd_bf16_d%d_%s%s", head_dim, cz,
              pack == 4 ? "_g4" : pack == 8 ? "_g8" : w8 ? "_w8" : "");
     void* args[] = {&q, &k, &v, &o, &l, &n_ctx_q, &n_ctx_k, &scale, &hq, &hkv, &nmb, &tot,
-                    &o_merged};
+                    &o_merged, &rope_cs};
     const int threads = pack ? 64 * pack : 2 * bm;
     return launch(name, dim3(tot), dim3(threads), 0, stream, args);
   }
-  if (o_merged) return TEENY_ERR_UNSUPPORTED;
+  if (o_merged || rope_cs) return TEENY_ERR_UNSUPPORTED;
   snprintf(name, sizeof name, "teeny_fa2_fwd_f32_d%d_%s", head_dim, cz);
   void* args[] = {&q, &k, &v, &o, &l, &n_ctx_q, &n_ctx_k, &scale, &hq, &hkv};
   return launch(name, dim3((n_ctx_q + 63) / 64, batch * hq), dim3(64), 0, stream, args);
@@ -582,6 +583,33 @@ int teeny_flash_attn2_fwd_merged(const void* q, const void* k, const void* v, vo
                  n_heads_q, n_heads_kv, head_dim, dtype, stream, 1);
 }
 
+int teeny_flash_attn2_fwd_qkv(const void* qkv, const float* rope_cs, const void* k, const void* v,
+                              void* o, float* l, int n_ctx_q, int n_ctx_k, float softmax_scale,
+                              float neg_inf, int batch, int n_heads_q, int n_heads_kv,
+                              int head_dim, int dtype, int causal, hipStream_t stream) {
+  if (dtype != TEENY_BF16) return TEENY_ERR_UNSUPPORTED;  // the bf16 kernels only
+  if (!rope_cs) return TEENY_ERR_NULL_POINTER;
+  if (reinterpret_cast<uintptr_t>(rope_cs) % 16 != 0) return TEENY_ERR_INVALID_VALUE;
+  if (n_heads_q > 0 && n_heads_kv > 0 && n_ctx_q > 0 && batch > 0 &&
+      (long)batch * n_ctx_q * (n_heads_q + 2 * n_heads_kv) * head_dim >= kMaxElems)
+    return TEENY_ERR_INVALID_SHAPE;
+  return fa2_fwd(causal != 0, qkv, k, v, o, l, n_ctx_q, n_ctx_k, softmax_scale, neg_inf, batch,
+                 n_heads_q, n_heads_kv, head_dim, dtype, stream, 1, rope_cs);
+}
+
+int teeny_rope_table(float* cs, int n_pos, int head_dim, float ln_rope_base,
+                     hipStream_t stream) {
+  if (!cs) return TEENY_ERR_NULL_POINTER;
+  if (n_pos <= 0 || n_pos % 32 != 0 || head_dim <= 0 || head_dim % 16 != 0 ||
+      (long)n_pos * head_dim >= kMaxElems)
+    return TEENY_ERR_INVALID_SHAPE;
+  if (!std::isfinite(ln_rope_base)) return TEENY_ERR_INVALID_VALUE;
+  const long n = (long)n_pos * (head_dim / 2);
+  void* args[] = {&cs, &n_pos, &head_dim, &ln_rope_base};
+  return launch("teeny_rope_table_f32", dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                args);
+}
+
 int teeny_causal_flash_attn2_bwd(const void* q, const void* k, const void* v, const void* o,
                                  const void* dout, const float* l, void* dq, void* dk, void* dv,
                                  int n_ctx_q, int n_ctx_k, float softmax_scale, int batch,
@@ -834,7 +862,7 @@ static int qkv_rope_split_check(const void* qkv, const void* q_out, const void* 
                                 const void* v_cache, int batch, int seq_len, int pos0,
                                 int cache_len, int n_heads_q, int n_heads_kv, int head_dim,
                                 float ln_rope_base, int dtype) {
-  if (!qkv || !q_out || !k_cache || !v_cache) return TEENY_ERR_NULL_POINTER;
+  if (!qkv || !k_cache || !v_cache) return TEENY_ERR_NULL_POINTER;
   if (!dtype_ok(dtype)) return TEENY_ERR_UNSUPPORTED;
   if (batch <= 0 || seq_len <= 0 || pos0 < 0 || n_heads_q <= 0 || n_heads_kv <= 0 ||
       n_heads_q % n_heads_kv != 0 || head_dim <= 0 || cache_len < pos0 + seq_len ||
@@ -859,9 +887,10 @@ static int qkv_rope_split_impl(const void* qkv, void* q_out, void* k_cache, void
   int rc = qkv_rope_split_check(qkv, q_out, k_cache, v_cache, batch, seq_len, pos0, cache_len,
                                 n_heads_q, n_heads_kv, head_dim, ln_rope_base, dtype);
   if (rc) return rc;
-  const int htot = n_heads_q + 2 * n_heads_kv;
-  // 256 threads: (256 / vectors per row) positions x 8 head rows each
-  const long gy = (long)batch * ((htot + 7) / 8);
+  // 256 threads: (256 / vectors per row) positions x 8 head rows each; no
+  // q_out: the K and V head rows only
+  const int rows = q_out ? n_heads_q + 2 * n_heads_kv : 2 * n_heads_kv;
+  const long gy = (long)batch * ((rows + 7) / 8);
   const int ppw = 256 / (head_dim / (dtype == TEENY_BF16 ? 8 : 4));
   char name[48];
   snprintf(name, sizeof name, "teeny_qkv_rope_split_%s", dtype_tag(dtype));
@@ -892,7 +921,7 @@ int teeny_qkv_rope_split_partials_dev(const float* parts, int n_parts, void* q_o
                                       const int32_t* pos0, int cache_len, int n_heads_q,
                                       int n_heads_kv, int head_dim, float ln_rope_base,
                                       int dtype, hipStream_t stream) {
-  if (!parts || !pos0) return TEENY_ERR_NULL_POINTER;
+  if (!parts || !pos0 || !q_out) return TEENY_ERR_NULL_POINTER;
   if (n_parts <= 0) return TEENY_ERR_INVALID_SHAPE;
   // shape checks on a stand-in qkv pointer, then the partial-input kernel
   int rc = qkv_rope_split_check(parts, q_out, k_cache, v_cache, batch, seq_len, 0, cache_len,

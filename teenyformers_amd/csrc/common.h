@@ -37,6 +37,23 @@ DEVI uint32_t pack_bf16x2(float lo, float hi) {
 DEVI float bf16lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 DEVI float bf16hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
+// RoPE of interleaved pairs (src/kernels/rope.rs:57-97, 86-88): pair k of a
+// row at position pos turns by theta = fp32(pos) * fp32(exp_f64(fp32(k) * c))
+// with c = (-2 ln_base) / head_dim in fp32.  Every kernel that rotates takes
+// its (cos, sin) from rope_cos_sin and rotates with rope_rotate, so that the
+// same row at the same position gets the same bits in each of them.
+DEVI float rope_c(float ln_base, int head_dim) { return (-2.0f * ln_base) / (float)head_dim; }
+DEVI void rope_cos_sin(int pos, int k, float c, float& cn, float& sn) {
+  const float inv = (float)exp((double)((float)k * c));
+  sincosf((float)pos * inv, &sn, &cn);
+}
+// (x0, x1) -> (x0 cos - x1 sin, x0 sin + x1 cos): the second product of each
+// rounded, the first fused with the sum
+DEVI void rope_rotate(float x0, float x1, float cn, float sn, float& o0, float& o1) {
+  o0 = __builtin_fmaf(x0, cn, -(x1 * sn));
+  o1 = __builtin_fmaf(x0, sn, x1 * cn);
+}
+
 // Generic element load/store with fp32 arithmetic.
 template <typename T> DEVI float ld(const T* p) { return (float)*p; }
 template <typename T> DEVI void st(T* p, float v) { *p = (T)v; }

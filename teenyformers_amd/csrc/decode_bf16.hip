@@ -293,10 +293,8 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
   }
   if (tid >= NT - D / 2) {
     const int kk = tid - (NT - D / 2);
-    const float c = (-2.0f * ln_base) / (float)D;
-    const float inv = (float)exp((double)((float)kk * c));
     float sn, cn;
-    sincosf((float)pos * inv, &sn, &cn);
+    rope_cos_sin(pos, kk, rope_c(ln_base, D), cn, sn);
     sm.cs[kk][0] = cn;
     sm.cs[kk][1] = sn;
   }
@@ -315,8 +313,7 @@ __device__ void decode_qkv_attn(const float* __restrict__ parts, int n_parts, lo
         for (int j = 0; j < VN / 2; ++j) {
           const int kk = vv * (VN / 2) + j;
           const float cn = sm.cs[kk][0], sn = sm.cs[kk][1];
-          out[2 * j] = in[r][2 * j] * cn - in[r][2 * j + 1] * sn;
-          out[2 * j + 1] = in[r][2 * j] * sn + in[r][2 * j + 1] * cn;
+          rope_rotate(in[r][2 * j], in[r][2 * j + 1], cn, sn, out[2 * j], out[2 * j + 1]);
         }
       } else {
 #pragma unroll

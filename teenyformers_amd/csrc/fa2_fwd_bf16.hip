@@ -71,7 +71,8 @@ template <int D, bool CAUSAL, int NW = 4, bool PACK = false, int NSUB = 2>
 __device__ __forceinline__ void fa2_fwd_bf16(const bf16* __restrict__ q, const bf16* __restrict__ k,
                              const bf16* __restrict__ v, bf16* __restrict__ o,
                              float* __restrict__ lse, int nq, int nk, float scale, int hq, int hkv,
-                             int num_m_blocks, int total_blocks, int o_merged) {
+                             int num_m_blocks, int total_blocks, int o_merged,
+                             const float2* __restrict__ rope_cs) {
   constexpr int BN = SUBN * NSUB;      // keys per tile
   constexpr int BM = 32 * NW;          // query rows per workgroup
   constexpr int NT = 64 * NW;          // threads
@@ -121,13 +122,53 @@ __device__ __forceinline__ void fa2_fwd_bf16(const bf16* __restrict__ q, const b
   const bf16* vb = v + kvh * (long)nk * D;
 
   // ---- Q rows -> registers (B operand) -------------------------------------
-  // rows past nq load row nq - 1: computed, never stored
+  // rows past nq load row nq - 1: computed, never stored.  rope_cs: q is the
+  // fused QKV projection [B, nq, (hq + 2 hkv) D], whose q heads are rotated
+  // here (row r at position r, the (cos, sin) of cs row r) as the split
+  // kernel would rotate them, and rounded to bf16 as it would store them
   bf16x8 qreg[DC];
+  // rope_cs: the (cos, sin) of the lane's pairs (columns 16 c + 8 g .. + 7
+  // are pairs 8 c + 4 g .. + 3: two float4 per c, pairs 8 c + 4 g + 2 m,
+  // +1 in qcs[2 c + m]), applied once the first tiles are requested, so
+  // that their loads do not wait for Q's
+  float4 qcs[2 * DC];
   {
-    const bf16* qp = q + ((long)bhq * nq + min(qrow, nq - 1)) * D + 8 * g;
+    const int qr = min(qrow, nq - 1);
+    const bf16* qp;
+    if (rope_cs) {
+      const int qb = bhq / hq, qh = bhq - qb * hq;
+      qp = q + ((long)qb * nq + qr) * ((hq + 2 * hkv) * D) + qh * D + 8 * g;
+    } else {
+      qp = q + ((long)bhq * nq + qr) * D + 8 * g;
+    }
 #pragma unroll
     for (int c = 0; c < DC; ++c) qreg[c] = as_bf16x8(*reinterpret_cast<const u32x4*>(qp + 16 * c));
+    if (rope_cs) {
+      // the table's row blocks of 32 positions: load i of the lane (row qr,
+      // half g) is float4 ((qr / 32) * 2 DC + i) * 64 + (qr % 32) * 2 + g,
+      // one KiB per load instruction of the wavefront
+      const float4* cs = reinterpret_cast<const float4*>(rope_cs) +
+                         (long)(qr >> 5) * (2 * DC * 64) + (qr & 31) * 2 + g;
+#pragma unroll
+      for (int i = 0; i < 2 * DC; ++i) qcs[i] = cs[64 * i];
+    }
   }
+  auto rotate_q = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      const u32x4 w = __builtin_bit_cast(u32x4, qreg[c]);
+      u32x4 r;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 t = qcs[2 * c + j / 2];  // (cos, sin) of pairs 2 (j / 2), +1
+        const float cn = j % 2 ? t.z : t.x, sn = j % 2 ? t.w : t.y;
+        float o0, o1;
+        rope_rotate(bf16lo(w[j]), bf16hi(w[j]), cn, sn, o0, o1);
+        r[j] = pack_bf16x2(o0, o1);
+      }
+      qreg[c] = as_bf16x8(r);
+    }
+  };
 
   int kend = nk;
   if (CAUSAL) kend = min(nk, blk_end);
@@ -355,6 +396,7 @@ __device__ __forceinline__ void fa2_fwd_bf16(const bf16* __restrict__ q, const b
     }
     // (the barrier alone: __syncthreads would wait for tile 1's loads too)
     barrier_only();
+    if (rope_cs) rotate_q();
     f32x16 s0, s1;
     qk(sm.k[0], s0, s1);
     mask(0, s0, s1);
@@ -528,9 +570,10 @@ __device__ __forceinline__ void fa2_fwd_bf16(const bf16* __restrict__ q, const b
   extern "C" __global__ __launch_bounds__(64 * NW)                                               \
       __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void teeny_fa2_fwd_bf16_d##D##_##SFX(       \
           const bf16* q, const bf16* k, const bf16* v, bf16* o, float* l, int nq, int nk,        \
-          float scale, int hq, int hkv, int nmb, int total, int o_merged) {                      \
+          float scale, int hq, int hkv, int nmb, int total, int o_merged,                       \
+          const float2* rope_cs) {                                                               \
     fa2_fwd_bf16<D, C, NW, PACK, NSUB>(q, k, v, o, l, nq, nk, scale, hq, hkv, nmb, total,        \
-                                       o_merged);                                                \
+                                       o_merged, rope_cs);                                       \
   }
 
 // 4 wavefronts, 128 query rows of one (b, q head) per workgroup

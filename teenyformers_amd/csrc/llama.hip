@@ -9,7 +9,9 @@
 //   fp32(exp_f64(fp32(k) * (-2 ln_base / D))), position = absolute position.
 //   pos0 may instead be read from device memory (a captured decode step whose
 //   position advances between replays); rows whose position falls outside
-//   the cache are then not written to it.
+//   the cache are then not written to it.  With q_out null only the cache
+//   rows are written (the bf16 prompt attention then reads Q from qkv and
+//   rotates it as it loads it, with teeny_rope_table's (cos, sin)).
 //
 // teeny_decode_attn_*: one new query row per (b, q head) against the first
 //   n_keys cached keys (flash-decoding: split-K partials over 256-key chunks,
@@ -67,14 +69,12 @@ __device__ void qkv_rope_split(const T* __restrict__ qkv, T* __restrict__ q_out,
   if (first) load(v, hh, s, in);
 
   if (pos_dev) pos0 += *pos_dev;
-  const float c = (-2.0f * ln_base) / (float)head_dim;
+  const float c = rope_c(ln_base, head_dim);
   for (int i = threadIdx.x; i < kPos * half; i += kThreads) {
     int pp = i / half, k = i - pp * half;
     if (s0 + pp >= seq) break;  // i grows with pp: no later entry is needed either
-    float inv = (float)exp((double)((float)k * c));
-    float theta = (float)(pos0 + s0 + pp) * inv;
     float sn, cn;
-    sincosf(theta, &sn, &cn);
+    rope_cos_sin(pos0 + s0 + pp, k, c, cn, sn);
     cs_tab[i] = make_float2(cn, sn);
   }
   __syncthreads();
@@ -98,9 +98,7 @@ __device__ void qkv_rope_split(const T* __restrict__ qkv, T* __restrict__ q_out,
       const float2* cs = cs_tab + p * half + v * (VN / 2);
 #pragma unroll
       for (int j = 0; j < VN / 2; ++j) {
-        float x0 = in[2 * j], x1 = in[2 * j + 1];
-        out[2 * j] = x0 * cs[j].x - x1 * cs[j].y;
-        out[2 * j + 1] = x0 * cs[j].y + x1 * cs[j].x;
+        rope_rotate(in[2 * j], in[2 * j + 1], cs[j].x, cs[j].y, out[2 * j], out[2 * j + 1]);
       }
     } else {
 #pragma unroll
@@ -131,9 +129,11 @@ __device__ void qkv_rope_rows(const T* __restrict__ qkv, T* __restrict__ q_out,
   const int v = threadIdx.x % vpr;
   const int s = blockIdx.x * ppw + threadIdx.x / vpr;
   const int htot = hq + 2 * hkv;
-  const int groups = (htot + kQkvHeads - 1) / kQkvHeads;
+  // q_out null: the K and V rows only (the attention reads Q from qkv itself)
+  const int hbase = q_out ? 0 : hq;
+  const int groups = (htot - hbase + kQkvHeads - 1) / kQkvHeads;
   const int b = blockIdx.y / groups;
-  const int h0 = (blockIdx.y - b * groups) * kQkvHeads;
+  const int h0 = hbase + (blockIdx.y - b * groups) * kQkvHeads;
   if (s >= seq || (int)threadIdx.x >= ppw * vpr) return;
   const T* src = qkv + (((long)b * seq + s) * htot + h0) * head_dim + v * VN;
   float in[kQkvHeads][VN];
@@ -145,13 +145,9 @@ __device__ void qkv_rope_rows(const T* __restrict__ qkv, T* __restrict__ q_out,
   const int pos = pos0 + s;
   float cn[VN / 2], sn[VN / 2];
   if (h0 < hq + hkv) {  // some head of the group is rotated
-    const float c = (-2.0f * ln_base) / (float)head_dim;
+    const float c = rope_c(ln_base, head_dim);
 #pragma unroll
-    for (int j = 0; j < VN / 2; ++j) {
-      const int k = v * (VN / 2) + j;
-      const float inv = (float)exp((double)((float)k * c));
-      sincosf((float)pos * inv, &sn[j], &cn[j]);
-    }
+    for (int j = 0; j < VN / 2; ++j) rope_cos_sin(pos, v * (VN / 2) + j, c, cn[j], sn[j]);
   }
 #pragma unroll
   for (int h = 0; h < kQkvHeads; ++h) {
@@ -169,9 +165,7 @@ __device__ void qkv_rope_rows(const T* __restrict__ qkv, T* __restrict__ q_out,
     if (hh < hq + hkv) {
 #pragma unroll
       for (int j = 0; j < VN / 2; ++j) {
-        const float x0 = in[h][2 * j], x1 = in[h][2 * j + 1];
-        out[2 * j] = x0 * cn[j] - x1 * sn[j];
-        out[2 * j + 1] = x0 * sn[j] + x1 * cn[j];
+        rope_rotate(in[h][2 * j], in[h][2 * j + 1], cn[j], sn[j], out[2 * j], out[2 * j + 1]);
       }
     } else {
 #pragma unroll
@@ -448,7 +442,33 @@ __device__ void argmax_rows(const T* __restrict__ x, long long* __restrict__ out
   }
 }
 
+// The (cos, sin) of every pair at positions 0 .. n_pos - 1 (n_pos a multiple
+// of 32), what the kernels above evaluate for a row at that position, laid
+// out for the bf16 forward's Q load: a lane of row r (r % 32 = lane % 32)
+// and half g (lane / 32) rotates pairs 8 c + 4 g + 2 m + e (e, m in 0..1, c
+// < head_dim / 16), and its load i = 2 c + m is the 16 bytes
+// (cos, sin, cos, sin) of pairs e = 0, 1 at float4 index
+// ((r / 32) * (head_dim / 8) + i) * 64 + (r % 32) * 2 + g, so that one load
+// instruction of a wavefront reads one contiguous KiB.
+__device__ void rope_table(float2* __restrict__ cs, int n_pos, int head_dim, float ln_base) {
+  const int half = head_dim / 2;
+  const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (long)n_pos * half) return;
+  const int p = (int)(t / half), k = (int)(t - (long)p * half);
+  float cn, sn;
+  rope_cos_sin(p, k, rope_c(ln_base, head_dim), cn, sn);
+  const int c = k >> 3, g = (k >> 2) & 1, m = (k >> 1) & 1, e = k & 1;
+  const long f4 = ((long)(p >> 5) * (head_dim / 8) + 2 * c + m) * 64 + (p & 31) * 2 + g;
+  cs[2 * f4 + e] = make_float2(cn, sn);
+}
+
 }  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void teeny_rope_table_f32(float2* cs, int n_pos,
+                                                                       int head_dim,
+                                                                       float ln_base) {
+  rope_table(cs, n_pos, head_dim, ln_base);
+}
 
 #define TEENY_QKV_PARTS_INST(TN, T)                                                             \
   extern "C" __global__ __launch_bounds__(256) void teeny_qkv_parts_rope_split_##TN(           \

@@ -39,13 +39,11 @@ __device__ void rope_rows(const T* __restrict__ x, T* __restrict__ y, int bh_tot
   for (int h = 0; h < kHeads; ++h)
     if (bh0 + h < bh_total) Vec16<T>::load(x + off0 + h * hstride, in[h]);
 
-  const float c = (-2.0f * ln_base) / (float)head_dim;
+  const float c = rope_c(ln_base, head_dim);
   float cn[VN / 2], sn[VN / 2];
 #pragma unroll
   for (int j = 0; j < VN / 2; ++j) {
-    const int k = v * (VN / 2) + j;
-    const float inv = (float)exp((double)((float)k * c));
-    sincosf((float)s * inv, &sn[j], &cn[j]);
+    rope_cos_sin(s, v * (VN / 2) + j, c, cn[j], sn[j]);
     if (backward) sn[j] = -sn[j];
   }
 #pragma unroll
@@ -54,9 +52,7 @@ __device__ void rope_rows(const T* __restrict__ x, T* __restrict__ y, int bh_tot
     float out[VN];
 #pragma unroll
     for (int j = 0; j < VN / 2; ++j) {
-      const float x0 = in[h][2 * j], x1 = in[h][2 * j + 1];
-      out[2 * j] = x0 * cn[j] - x1 * sn[j];
-      out[2 * j + 1] = x0 * sn[j] + x1 * cn[j];
+      rope_rotate(in[h][2 * j], in[h][2 * j + 1], cn[j], sn[j], out[2 * j], out[2 * j + 1]);
     }
     Vec16<T>::store(y + off0 + h * hstride, out);
   }

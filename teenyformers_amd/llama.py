@@ -179,6 +179,7 @@ class Llama:
         self.w = weights
         self.decode_ws = None
         self.sw = {}  # streaming-layout copies of the decode weights (stream_layout)
+        self._cs = None  # RoPE (cos, sin) table of the bf16 prompt attention
 
     def stream_layout(self) -> "Llama":
         """Give the weights that one-token steps stream (each layer's qkv, o,
@@ -222,6 +223,17 @@ class Llama:
             o = ops.decode_qkv_attention(qkv, cache.k[i], cache.v[i], pos0, Hq, Hkv,
                                          cfg.rope_base, scale)
             return ops.linear_split(o.view(B, 1, Hq * D), self._lw(p + "o_proj.weight"))
+        if (not isinstance(pos0, torch.Tensor) and pos0 == 0
+                and not isinstance(qkv, ops.Partials) and qkv.dtype == torch.bfloat16):
+            # bf16 prompt: K and V into the cache; the attention reads the q
+            # heads from qkv, rotates them as it loads them and writes the
+            # merged-heads layout (the same bits as the split into a Q
+            # buffer, the forward and merge_heads, with Q and O written and
+            # read once fewer)
+            ops.qkv_rope_split(qkv, None, cache.k[i], cache.v[i], 0, Hq, Hkv, cfg.rope_base)
+            att, _ = ops.flash_attn2_fwd_qkv(qkv, self._rope_table(S, n1.device), cache.k[i],
+                                             cache.v[i], Hq, scale, causal=True)
+            return ops.linear_split(att, self._lw(p + "o_proj.weight"))
         q = torch.empty((B, Hq, S, D), dtype=n1.dtype, device=n1.device)
         ops.qkv_rope_split(qkv, q, cache.k[i], cache.v[i], pos0, Hq, Hkv, cfg.rope_base)
         if isinstance(pos0, torch.Tensor):  # graph decode: the position is on the device
@@ -247,6 +259,15 @@ class Llama:
         # one position: [B, Hq, 1, D] is already the merged [B, 1, Hq D] layout
         att = o.view(B, S, Hq * D) if S == 1 else ops.merge_heads(o)
         return ops.linear_split(att, self._lw(p + "o_proj.weight"))
+
+    def _rope_table(self, n: int, device) -> torch.Tensor:
+        """RoPE's (cos, sin) for positions 0 .. n-1 at least (kept, grown to
+        a power of two)."""
+        cs, D = self._cs, self.cfg.head_dim()
+        if cs is None or cs.numel() < n * D or cs.device != device:
+            m = max(32, 1 << max(0, n - 1).bit_length())
+            cs = self._cs = ops.rope_table(m, D, self.cfg.rope_base, device)
+        return cs
 
     def _fused_decode(self, qkv, cache: KVCache) -> bool:
         """Whether a one-token step runs teeny_decode_qkv_attention_dev: bf16

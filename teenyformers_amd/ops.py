@@ -105,6 +105,51 @@ def flash_attn2_fwd_merged(q, k, v, softmax_scale: float | None = None, causal: 
     return out, lse
 
 
+def rope_table(n_pos: int, head_dim: int, rope_base: float, device) -> torch.Tensor:
+    """(cos, sin) of RoPE's pairs at positions 0 .. n_pos-1 (rounded up to 32)
+    in the order flash_attn2_fwd_qkv loads them (teeny_rope_table): a flat
+    fp32 tensor of n_pos * head_dim values; rope_table_pairs gives the
+    [n_pos, D/2, 2] view."""
+    n = (n_pos + 31) // 32 * 32
+    cs = torch.empty(n * head_dim, dtype=torch.float32, device=device)
+    call("teeny_rope_table", _p(cs), n, head_dim, _ln(rope_base), _stream())
+    return cs
+
+
+def rope_table_pairs(cs: torch.Tensor, head_dim: int) -> torch.Tensor:
+    """[n_pos, D/2, 2] (cos, sin) of a rope_table: pair k = 8c + 4g + 2m + e of
+    position p sits in float4 ((p/32) (D/8) + 2c + m) 64 + (p%32) 2 + g."""
+    D = head_dim
+    t = cs.view(-1, D // 8, 32, 2, 2, 2)      # [p/32, i = 2c + m, p%32, g, e, (cos, sin)]
+    t = t.view(-1, D // 16, 2, 32, 2, 2, 2)   # [p/32, c, m, p%32, g, e, cs]
+    t = t.permute(0, 3, 1, 4, 2, 5, 6)        # [p/32, p%32, c, g, m, e, cs]
+    return t.reshape(-1, D // 2, 2)
+
+
+def flash_attn2_fwd_qkv(qkv, rope_cs, k, v, n_heads_q: int, softmax_scale: float | None = None,
+                        causal: bool = True):
+    """The prompt attention straight from the fused QKV projection: qkv
+    [B, S, (Hq+2Hkv)*D] bf16 (its q heads rotated as they load, row r at
+    position r with rope_cs row r), k/v [B, Hkv, Sk, D] (the cache);
+    returns o [B, S, Hq*D] (merged heads) and lse [B, Hq, S]."""
+    _dev(qkv, rope_cs, k, v)
+    B, S, W = qkv.shape
+    _, Hkv, Sk, D = k.shape
+    Hq = n_heads_q
+    if W != (Hq + 2 * Hkv) * D or v.shape != k.shape or k.shape[0] != B:
+        raise ValueError("qkv must be [B, S, (Hq+2Hkv)*D] matching k, v [B, Hkv, Sk, D]")
+    if not (qkv.dtype == k.dtype == v.dtype == torch.bfloat16):
+        raise TypeError("flash_attn2_fwd_qkv: bf16 qkv, k, v")
+    if rope_cs.dtype != torch.float32 or rope_cs.numel() < (S + 31) // 32 * 32 * D:
+        raise ValueError("rope_cs: a rope_table of at least S positions")
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    out = torch.empty((B, S, Hq * D), dtype=qkv.dtype, device=qkv.device)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device=qkv.device)
+    call("teeny_flash_attn2_fwd_qkv", _p(qkv), _p(rope_cs), _p(k), _p(v), _p(out), _p(lse), S, Sk,
+         scale, float("-inf"), B, Hq, Hkv, D, _code(qkv), int(bool(causal)), _stream())
+    return out, lse
+
+
 def flash_attn2_bwd_workspace_bytes(q: torch.Tensor, k: torch.Tensor | None = None) -> int:
     """Backward workspace; given k, the size that also allows the GQA head
     split of the dK/dV kernel where it applies."""
@@ -401,7 +446,7 @@ def qkv_rope_split(qkv, q_out, k_cache, v_cache, pos0, n_heads_q: int, n_heads_k
     """qkv [B, S, (Hq+2Hkv)*D] -> q_out [B, Hq, S, D] (RoPE) and K (RoPE) / V
     written to caches [B, Hkv, L, D] at rows pos0 .. pos0+S-1.  pos0: an int,
     or a one-element int32 device tensor read when the kernel runs (for
-    captured graphs)."""
+    captured graphs).  q_out None (a dense qkv only): the caches only."""
     if isinstance(qkv, Partials):
         _dev(qkv.slabs, q_out, k_cache, v_cache)
         B, S, _ = qkv.shape
@@ -416,7 +461,7 @@ def qkv_rope_split(qkv, q_out, k_cache, v_cache, pos0, n_heads_q: int, n_heads_k
         return
     _dev(qkv, q_out, k_cache, v_cache)
     B, S, _ = qkv.shape
-    D = q_out.shape[-1]
+    D = k_cache.shape[-1]
     if isinstance(pos0, torch.Tensor):
         if pos0.dtype != torch.int32 or not pos0.is_cuda:
             raise TypeError("a device position must be an int32 CUDA tensor")

@@ -67,6 +67,29 @@ def test_fa2_fwd_merged_validation(L):
         assert m(c, scale=0.0) == VALUE
 
 
+def test_fa2_fwd_qkv_and_rope_table_validation(L):
+    """The attention from the fused QKV projection validates like the
+    forward, is bf16 only and needs a 16-byte aligned (cos, sin) table."""
+    def f(**kw):
+        a = dict(qkv=P, cs=P, nq=128, dtype=BF16, scale=0.125, d=64)
+        a.update(kw)
+        return L.teeny_flash_attn2_fwd_qkv(a["qkv"], a["cs"], P, P, P, P, a["nq"], 128, a["scale"],
+                                           NEG_INF, 1, 4, 2, a["d"], a["dtype"], 1, None)
+    assert f(dtype=F32) == UNSUP
+    assert f(cs=None) == NULLP
+    assert f(cs=P + 8) == VALUE
+    assert f(qkv=None) == NULLP
+    assert f(nq=0) == SHAPE
+    assert f(d=96) == UNSUP
+    assert f(scale=0.0) == VALUE
+    assert f(nq=1 << 22, d=128) == SHAPE  # B*S*(Hq+2Hkv)*D past the 32-bit element range
+    assert L.teeny_rope_table(None, 16, 64, 9.2, None) == NULLP
+    assert L.teeny_rope_table(P, 0, 64, 9.2, None) == SHAPE
+    assert L.teeny_rope_table(P, 16, 64, 9.2, None) == SHAPE  # positions in blocks of 32
+    assert L.teeny_rope_table(P, 32, 40, 9.2, None) == SHAPE  # head_dim a multiple of 16
+    assert L.teeny_rope_table(P, 32, 64, float("inf"), None) == VALUE
+
+
 def test_fa2_scale_domain(L):
     """bf16 kernels fold the scale into the exponent after masking raw
     scores to -inf: scale must be > 0 there (0 or negative would turn masked

@@ -201,6 +201,59 @@ def test_fa2_bf16_fwd_merged(cuda, shape, causal):
     assert torch.equal(lm.view(torch.int32), lse.view(torch.int32))
 
 
+QKV_SHAPES = [  # B, Hq, Hkv, S, cache length, D
+    (16, 32, 8, 512, 640, 128),   # the Llama-3-8B prefill (GQA 4 packed)
+    (4, 32, 8, 2048, 2048, 64),   # the Llama block
+    (2, 8, 8, 300, 320, 128),     # MHA: the 4-wavefront form, ragged
+    (1, 16, 2, 333, 400, 128),    # GQA 8 packed
+    (1, 8, 2, 8200, 8200, 128),   # the 8-wavefront form (8000+ rows)
+    (3, 4, 1, 1, 64, 64),         # one prompt row
+]
+
+
+@pytest.mark.parametrize("shape", QKV_SHAPES)
+@pytest.mark.parametrize("causal", [True, False])
+def test_fa2_bf16_fwd_qkv(cuda, shape, causal):
+    """The prompt attention from the fused QKV projection (its q heads
+    rotated as they load, with the RoPE table's (cos, sin)) gives the bits of
+    the split into a Q buffer followed by the merged-heads forward; the split
+    without q_out writes the same cache rows and nothing else."""
+    B, Hq, Hkv, S, L, D = shape
+    base = 5e5
+    g = torch.Generator(device="cuda").manual_seed(S + Hq + D)
+    qkv = torch.randn((B, S, (Hq + 2 * Hkv) * D), generator=g, device="cuda").to(torch.bfloat16)
+    kc1 = torch.zeros((B, Hkv, L, D), dtype=torch.bfloat16, device="cuda")
+    vc1, kc2, vc2 = torch.zeros_like(kc1), torch.zeros_like(kc1), torch.zeros_like(kc1)
+    q = torch.empty((B, Hq, S, D), dtype=torch.bfloat16, device="cuda")
+    ops.qkv_rope_split(qkv, q, kc1, vc1, 0, Hq, Hkv, base)
+    ops.qkv_rope_split(qkv, None, kc2, vc2, 0, Hq, Hkv, base)
+    scale = 1.0 / math.sqrt(D)
+    o1, l1 = ops.flash_attn2_fwd_merged(q, kc1, vc1, scale, causal)
+    cs = ops.rope_table(S + 3, D, base, "cuda")
+    o2, l2 = ops.flash_attn2_fwd_qkv(qkv, cs, kc2, vc2, Hq, scale, causal)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1.view(torch.int16), kc2.view(torch.int16))
+    assert torch.equal(vc1.view(torch.int16), vc2.view(torch.int16))
+    assert torch.equal(o2.view(torch.int16), o1.view(torch.int16))
+    assert torch.equal(l2.view(torch.int32), l1.view(torch.int32))
+
+
+def test_rope_table_values(cuda):
+    """teeny_rope_table against the angle of rope.rs:86-88 formed as the
+    oracle forms it (fp32 theta = fp32(pos) * fp32(exp(fp32(k * c)))), its
+    cos and sin taken in float64: within a few fp32 ulps of 1."""
+    n, D, base = 4100, 128, 5e5
+    cs = ops.rope_table_pairs(ops.rope_table(n, D, base, "cuda"), D).cpu().numpy()
+    assert cs.shape == (4128, D // 2, 2)
+    cs = cs[:n].astype(np.float64)
+    c = np.float32(np.float32(-2.0) * np.float32(ops._ln(base))) / np.float32(D)
+    kc = (np.arange(D // 2, dtype=np.float32) * c).astype(np.float64)
+    inv = np.exp(kc).astype(np.float32)
+    theta = (np.arange(n, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float64)
+    err = np.maximum(np.abs(cs[..., 0] - np.cos(theta)), np.abs(cs[..., 1] - np.sin(theta)))
+    assert float(err.max()) <= 2.5e-7, float(err.max())
+
+
 def test_fa2_fwd_merged_rejects_f32(cuda):
     q = torch.zeros((1, 2, 8, 64), device="cuda")
     with pytest.raises(TypeError):
