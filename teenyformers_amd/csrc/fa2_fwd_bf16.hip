@@ -43,7 +43,10 @@
 //     tiles are masked;
 //   * GQA: q head h reads kv head h / (Hq / Hkv);
 //   * scheduling: block ids are remapped so one XCD works through whole heads
-//     (K/V stay in that XCD's L2), heaviest causal blocks first.
+//     (K/V stay in that XCD's L2), heaviest causal blocks first;
+//   * o_merged: O is stored [B, Sq, Hq * D] (MergeHeadsOp fused, rows Hq D
+//     apart) instead of [B, Hq, Sq, D]; rope_cs: Q is read from the fused
+//     QKV projection and rotated (RoPE) as it is loaded.
 #include "cdna4.h"
 
 #include <type_traits>
@@ -124,7 +127,7 @@ __device__ __forceinline__ void fa2_fwd_bf16(const bf16* __restrict__ q, const b
   // ---- Q rows -> registers (B operand) -------------------------------------
   // rows past nq load row nq - 1: computed, never stored.  rope_cs: q is the
   // fused QKV projection [B, nq, (hq + 2 hkv) D], whose q heads are rotated
-  // here (row r at position r, the (cos, sin) of cs row r) as the split
+  // here (row r at position r, its (cos, sin) from the table) as the split
   // kernel would rotate them, and rounded to bf16 as it would store them
   bf16x8 qreg[DC];
   // rope_cs: the (cos, sin) of the lane's pairs (columns 16 c + 8 g .. + 7
