@@ -426,8 +426,15 @@ int fa2_bwd(bool causal, const void* q, const void* k, const void* v, const void
     tot = (int)total;
     snprintf(name, sizeof name, "teeny_fa2_bwd_dkdv_bf16_d%d_%s%s%s", head_dim, cz,
              plan.groups == 2 ? "_hg2" : "", gsfx);
+    // causal blocks all resident at once, two per CU: pair heavy key blocks
+    // with light ones on each CU (same-box A/B, same bits: B16 Hq32 Hkv8 S512
+    // 1.12x, B8 S1024 1.24x); the kernel's order needs whole heads and an
+    // even number of key blocks in each XCD's share
+    const int cus = device_cus();
+    int cu_pairs = causal && plan.groups == 1 && hsplit == 1 && tot > cus && tot <= 2 * cus &&
+                   tot % 8 == 0 && (tot / 8) % nnb == 0 && nnb % 2 == 0;
     void* a1[] = {&q,       &k,       &v,     &dout, &ld,  &dk,  &dv,  &n_ctx_q,
-                  &n_ctx_k, &scale,   &hq,    &hkv,  &nnb, &tot, &hsplit, &part};
+                  &n_ctx_k, &scale,   &hq,    &hkv,  &nnb, &tot, &hsplit, &part, &cu_pairs};
     rc = launch(name, dim3(tot), dim3(256 * plan.groups), 0, stream, a1);
     if (rc || hsplit == 1) return rc;
     long n = (long)batch * hkv * n_ctx_k * head_dim;  // a multiple of 8

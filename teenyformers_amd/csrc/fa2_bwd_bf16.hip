@@ -82,7 +82,7 @@ __device__ __forceinline__ void fa2_bwd_dkdv(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ dout, const float* __restrict__ ld, GT* __restrict__ dk,
     GT* __restrict__ dv, int nq, int nk, float scale, int hq, int hkv, int num_n_blocks,
-    int total_blocks, int hsplit, float* __restrict__ part, DkdvSmem<D>* smg) {
+    int total_blocks, int hsplit, float* __restrict__ part, int cu_pairs, DkdvSmem<D>* smg) {
   constexpr int DC = D / 16;            // d-chunks of 16 (QK^T, dO V^T)
   constexpr int DT = D / 32;            // d-tiles of 32 (dK^T, dV^T)
   constexpr int CPR = D / 8;            // 16-byte chunks per row
@@ -101,7 +101,21 @@ __device__ __forceinline__ void fa2_bwd_dkdv(
 
   const int id = xcd_remap(blockIdx.x, total_blocks);
   int hh, nb;  // hh = (b * hkv + hk) * hsplit + hs; key block 0 sees the most query rows
-  pair_order(id, num_n_blocks, total_blocks / num_n_blocks, hh, nb);
+  if (cu_pairs) {
+    // every workgroup resident at once, two per CU (the host checks the
+    // count and that each XCD's share holds whole heads and an even number
+    // of key blocks): an XCD's i-th and (i + half)-th workgroups were
+    // measured to share a CU, so the first half takes key blocks 0 ..
+    // nnb/2 - 1 and the second half the rest in reverse, pairing block r
+    // with block nnb - 1 - r and giving every CU about the same causal work
+    const int per_x = total_blocks / TEENY_NUM_XCD, hpx = per_x / num_n_blocks;
+    const int half = per_x / 2, x = id / per_x, L = id - x * per_x;
+    const int lp = L < half ? L : L - half;
+    hh = x * hpx + lp % hpx;
+    nb = L < half ? lp / hpx : num_n_blocks - 1 - lp / hpx;
+  } else {
+    pair_order(id, num_n_blocks, total_blocks / num_n_blocks, hh, nb);
+  }
   const int kvh = hh / hsplit, hs = hh - kvh * hsplit;
   const int b = kvh / hkv, hk = kvh - b * hkv;
   const int group = hq / hkv / hsplit / NG;  // q heads walked by this wavefront group
@@ -809,10 +823,10 @@ __device__ void fa2_bwd_dq(const bf16* __restrict__ q, const bf16* __restrict__ 
   void teeny_fa2_bwd_dkdv_bf16_d##D##_##CZ##SFX(                                                \
       const bf16* q, const bf16* k, const bf16* v, const bf16* dout, const float* ld, GT* dk,   \
       GT* dv, int nq, int nk, float scale, int hq, int hkv, int nnb, int total, int hsplit,     \
-      float* part) {                                                                            \
+      float* part, int cu_pairs) {                                                              \
     __shared__ DkdvSmem<D> sm[1];                                                               \
     fa2_bwd_dkdv<D, CAUSAL, GT>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb, total, \
-                                hsplit, part, sm);                                              \
+                                hsplit, part, cu_pairs, sm);                                    \
   }                                                                                             \
   extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
   void teeny_fa2_bwd_dq_bf16_d##D##_##CZ##SFX(                                                  \
@@ -839,14 +853,14 @@ TEENY_FA2_BWD_BF16_INST(128, n, false, float, _g32)
   void teeny_fa2_bwd_dkdv_bf16_d##D##_c_hg2##SFX(                                               \
       const bf16* q, const bf16* k, const bf16* v, const bf16* dout, const float* ld, GT* dk,   \
       GT* dv, int nq, int nk, float scale, int hq, int hkv, int nnb, int total, int hsplit,     \
-      float* part) {                                                                            \
+      float* part, int cu_pairs) {                                                              \
     __shared__ DkdvSmem<D> sm[2];                                                               \
     if (threadIdx.x >= 256)                                                                     \
       fa2_bwd_dkdv<D, true, GT, 2, 1>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb,  \
-                                      total, hsplit, part, sm);                                 \
+                                      total, hsplit, part, cu_pairs, sm);                       \
     else                                                                                        \
       fa2_bwd_dkdv<D, true, GT, 2, 0>(q, k, v, dout, ld, dk, dv, nq, nk, scale, hq, hkv, nnb,  \
-                                      total, hsplit, part, sm);                                 \
+                                      total, hsplit, part, cu_pairs, sm);                       \
   }
 
 TEENY_FA2_BWD_DKDV_HG2_INST(64, bf16, )

@@ -499,10 +499,12 @@ def test_fa2_bf16_c5_long_gqa(cuda, S):
     _group_check(1, 64, 8, S, 128, seed=8, spike=True, groups=[(0, 5)])
 
 
-@pytest.mark.parametrize("B,S,groups", [(2, 4096, [(1, 7)]), (16, 512, [(15, 3)])])
+@pytest.mark.parametrize("B,S,groups", [(2, 4096, [(1, 7)]), (16, 512, [(15, 3)]),
+                                         (8, 1024, [(0, 0), (7, 5)])])
 def test_fa2_bf16_gqa4_packed_group(cuda, B, S, groups):
     """Causal GQA groups of 4 (Hq32 Hkv8 D128), which run the GQA-packed
     forward and dQ: B2 S4096 (its dK/dV runs in two wavefront groups per
-    workgroup) and the Llama-3-8B prefill's B16 S512 (one group below 2048
-    rows); one whole group each, 1% of K rows x8."""
+    workgroup), the Llama-3-8B prefill's B16 S512 and B8 S1024 (below 2048
+    rows, all 512 dK/dV workgroups resident at once, heavy and light key
+    blocks paired on each CU); whole groups, 1% of K rows x8."""
     _group_check(B, 32, 8, S, 128, seed=9 + S, spike=True, groups=groups)
