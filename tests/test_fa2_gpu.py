@@ -508,3 +508,12 @@ def test_fa2_bf16_gqa4_packed_group(cuda, B, S, groups):
     rows, all 512 dK/dV workgroups resident at once, heavy and light key
     blocks paired on each CU); whole groups, 1% of K rows x8."""
     _group_check(B, 32, 8, S, 128, seed=9 + S, spike=True, groups=groups)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,groups", [(8, 32, 8, 1024, 64, [(3, 2)]),
+                                                 (2, 32, 32, 1024, 128, [(1, 31), (0, 0)])])
+def test_fa2_bf16_dkdv_cu_pairs(cuda, B, Hq, Hkv, S, D, groups):
+    """Causal shapes whose 512 dK/dV workgroups are all resident at once, so
+    the kernel pairs heavy and light key blocks on each CU: GQA 4 at D = 64
+    and MHA at D = 128; whole groups against the oracle."""
+    _group_check(B, Hq, Hkv, S, D, seed=11 + S + D, spike=True, groups=groups)
